@@ -1,0 +1,174 @@
+"""Benchmark: MoE route -> dispatch -> combine on one MI355X.
+
+A step is one pass of the whole path over one batch of synthetic input that
+is already resident in HBM: router GEMM + scoring/top-k + histogram
+(moe_route), stable permutation + gather (moe_permute), weighted combine
+(moe_combine).  Default workload: the DeepSeek-V3 shape (C4: T=32768,
+H=7168, E=256, top-8, sigmoid + bias, 8 groups keep 4, x2.5).
+
+Prints ONE JSON line: routed tokens/s, ms/step, the roofline of the dominant
+kernel (algorithmic bytes / HIP-event-timed launch duration vs 8 TB/s),
+per-stage times, the end-to-end HBM fraction, and the CPU oracle's rate on a
+bounded sample of the same workload (rank 0, N=1).
+
+    python bench.py [--steps K] [--warmup W] [--config C4|C5|C2|C3] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [REPO, os.path.join(REPO, "ernie-evolve-results_amd")]
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+import moe_route as M  # noqa: E402
+from moe_route.configs import CONFIGS  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def algorithmic_bytes(c):
+    """Bytes each stage must move at minimum (x read by the router and again
+    by the permute; each routed row written once and read once)."""
+    T, H, E, k = c.T, c.H, c.E, c.k
+    xb = 2
+    db = 1 if c.fp8 else 2
+    route = T * H * xb + E * H * 2 + T * E * 4 + T * k * 8
+    gather = T * H * xb + T * k * H * db + (T * k * (H // 128) * 4 if c.fp8 else 0) + T * k * 8
+    combine = T * k * H * 2 + T * H * 2 + T * k * 8
+    return dict(route=route, gather=gather, combine=combine, router_gemm=T * H * xb + E * H * 2
+                + T * E * 4)
+
+
+def cpu_baseline(c, sample_T):
+    """The CPU oracle (oracle/moe_oracle.py) on `sample_T` tokens of the same
+    workload: router GEMM (torch fp32), scoring/top-k, permutation, gather /
+    fp8 quantisation and combine.  1 warm-up + median of 3."""
+    from oracle import moe_oracle as O
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    x, w, bias, y = M.make_inputs(c, T=sample_T, seed=0)
+    cfg = O.RouteCfg(c.cfg.scoring, c.cfg.renormalize, c.cfg.n_group, c.cfg.topk_group,
+                     c.cfg.route_scale, c.cfg.norm_min)
+    b = None if bias is None else bias.numpy()
+
+    def once():
+        O.route_dispatch_combine(x, w, b, y, c.k, cfg, fp8=c.fp8)
+
+    once()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        once()
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    return {"value": sample_T / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": "%d tokens of %s (T,H,E,k = %d,%d,%d,%d), oracle route+permute+combine, "
+                      "median of 3 = %.3f s" % (sample_T, c.name, sample_T, c.H, c.E, c.k, med)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C4")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=8192)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this path runs on one GPU only (no sharding, no collectives); "
+              "--gpus %d is not supported" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    c = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
+    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, dev, fp8=c.fp8)
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        plan.step(x, w, bias, y)
+    torch.cuda.synchronize()
+
+    # ---- timed region: exactly K steps, whole path, inputs resident in HBM
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        plan.step(x, w, bias, y)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    # ---- per-stage HIP-event timing (same stream the kernels run on)
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    st = {"router_gemm": [], "route": [], "permute": [], "combine": []}
+    for _ in range(args.steps):
+        e = [ev() for _ in range(5)]
+        e[0].record()
+        plan.router_gemm(x, w)
+        e[1].record()
+        plan.route(x, w, bias)
+        e[2].record()
+        plan.permute(x)
+        e[3].record()
+        plan.combine(y)
+        e[4].record()
+        torch.cuda.synchronize()
+        st["router_gemm"].append(e[0].elapsed_time(e[1]) * 1e3)
+        st["route"].append(e[1].elapsed_time(e[2]) * 1e3)
+        st["permute"].append(e[2].elapsed_time(e[3]) * 1e3)
+        st["combine"].append(e[3].elapsed_time(e[4]) * 1e3)
+    us = {k2: statistics.mean(v) for k2, v in st.items()}
+
+    ab = algorithmic_bytes(c)
+    # dominant kernel: the single-launch combine or the permute's gather
+    # (permute = 3 small index kernels + the gather launch)
+    comb_gbs = ab["combine"] / (us["combine"] * 1e-6) / 1e9
+    roofline = {"kernel": "combine_kernel", "bound": "hbm", "achieved": round(comb_gbs, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(comb_gbs / HBM_PEAK_GBS, 4),
+                "traffic": None, "algorithmic_bytes": ab["combine"],
+                "avg_launch_us": round(us["combine"], 2)}
+    total_bytes = ab["route"] + ab["gather"] + ab["combine"]
+    e2e_gbs = total_bytes / (ms_per_step * 1e-3) / 1e9
+    flops = 2.0 * c.T * c.H * c.E
+    gemm = {"us": round(us["router_gemm"], 2),
+            "tflops": round(flops / (us["router_gemm"] * 1e-6) / 1e12, 1),
+            "mfma_frac": round(flops / (us["router_gemm"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "hbm_frac": round(ab["router_gemm"] / (us["router_gemm"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(c, args.cpu_tokens)
+
+    tok_s = c.T / (ms_per_step * 1e-3)
+    line = {
+        "metric": "routed tokens/sec + achieved HBM GB/s (% of peak) at DSV3 shape, 1 MI355X",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded randn inputs generated on the GPU)",
+        "config": {"workload": "%s route+dispatch+combine: %s" % (c.name, c.description),
+                   "T": c.T, "H": c.H, "E": c.E, "k": c.k, "fp8_dispatch": c.fp8},
+        "roofline": roofline,
+        "e2e_hbm": {"algorithmic_bytes": total_bytes, "achieved": round(e2e_gbs, 1),
+                    "unit": "GB/s", "frac": round(e2e_gbs / HBM_PEAK_GBS, 4)},
+        "stages_us": {k2: round(v, 2) for k2, v in us.items()},
+        "stage_hbm_frac": {
+            "route": round(ab["route"] / (us["route"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "permute": round(ab["gather"] / (us["permute"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "combine": round(comb_gbs / HBM_PEAK_GBS, 4)},
+        "router_gemm": gemm,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

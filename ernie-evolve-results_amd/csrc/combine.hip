@@ -1,0 +1,131 @@
+// Stage 5: weighted combine (un-permute), fp32 accumulate.
+//
+// Replaces combine_kernel (K:2365-2428):
+//   out[t] = cast(shared[t] + sum_j w[t,j] * y[pair_row[t,j]])
+// Each thread produces one 16-byte vector of one output row.  All k row
+// loads are issued before the reduction (the reference found serialising them
+// cost ~12% of bandwidth, K:2358-2363) and use non-temporal hints, since every
+// byte of y is read exactly once (K:2391-2404).
+#include "moe_common.h"
+
+namespace moe {
+
+// bf16 vector: 8 elements; fp32 vector: 4 elements.
+template <bool BF16>
+struct Vec;
+template <>
+struct Vec<true> {
+  static constexpr int N = 8;
+  static __device__ __forceinline__ void unpack(u32x4 v, float (&f)[8]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) { f[2 * q] = bf16lo(v[q]); f[2 * q + 1] = bf16hi(v[q]); }
+  }
+  static __device__ __forceinline__ u32x4 pack(const float (&f)[8]) {
+    u32x4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
+    return v;
+  }
+};
+template <>
+struct Vec<false> {
+  static constexpr int N = 4;
+  static __device__ __forceinline__ void unpack(u32x4 v, float (&f)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f[q] = __uint_as_float(v[q]);
+  }
+  static __device__ __forceinline__ u32x4 pack(const float (&f)[4]) {
+    u32x4 v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = __float_as_uint(f[q]);
+    return v;
+  }
+};
+
+template <int K, bool BF16>
+__global__ __launch_bounds__(256) void combine_kernel(const u32x4* __restrict__ y,
+                                                      const int* __restrict__ pair_row,
+                                                      const float* __restrict__ w,
+                                                      const u32x4* __restrict__ shared,
+                                                      int total, int nvec,
+                                                      u32x4* __restrict__ out) {
+  using VT = Vec<BF16>;
+  constexpr int NE = VT::N;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
+    const int t = i / nvec;
+    const int v = i - t * nvec;
+    int r[K];
+    float wk[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      r[j] = pair_row[(long long)t * K + j];
+      wk[j] = w[(long long)t * K + j];
+    }
+    u32x4 yv[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      yv[j] = (u32x4){0u, 0u, 0u, 0u};
+      if (r[j] >= 0) yv[j] = ld_nt(y + (long long)r[j] * nvec + v);
+    }
+    float acc[NE];
+    if (shared) {
+      VT::unpack(ld_nt(shared + i), acc);
+    } else {
+#pragma unroll
+      for (int e = 0; e < NE; ++e) acc[e] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      float f[NE];
+      VT::unpack(yv[j], f);
+      const float wj = r[j] >= 0 ? wk[j] : 0.0f;
+#pragma unroll
+      for (int e = 0; e < NE; ++e) acc[e] += wj * f[e];
+    }
+    st_nt(out + i, VT::pack(acc));
+  }
+}
+
+template <bool BF16>
+static hipError_t launch_combine_t(const void* y, const int32_t* pair_row, const float* w,
+                                   const void* shared, int total, int nvec, int k, void* out,
+                                   hipStream_t s) {
+  long long g = (total + 255) / 256;
+  if (g > 65536) g = 65536;
+  const dim3 grid((unsigned)g), blk(256);
+  const u32x4* ys = (const u32x4*)y;
+  const u32x4* sh = (const u32x4*)shared;
+  u32x4* o = (u32x4*)out;
+#define MOE_COMBINE_CASE(KK)                                                                  \
+  case KK:                                                                                    \
+    hipLaunchKernelGGL((combine_kernel<KK, BF16>), grid, blk, 0, s, ys, pair_row, w, sh, total, \
+                       nvec, o);                                                              \
+    break;
+  switch (k) {
+    MOE_COMBINE_CASE(1)
+    MOE_COMBINE_CASE(2)
+    MOE_COMBINE_CASE(3)
+    MOE_COMBINE_CASE(4)
+    MOE_COMBINE_CASE(5)
+    MOE_COMBINE_CASE(6)
+    MOE_COMBINE_CASE(7)
+    MOE_COMBINE_CASE(8)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef MOE_COMBINE_CASE
+  return hipGetLastError();
+}
+
+// y_dtype: 0 = bf16, 1 = fp32 (checked by the caller)
+hipError_t launch_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* w,
+                          const void* shared, int T, int H, int k, void* out, hipStream_t s) {
+  const int elem = y_dtype == 0 ? 2 : 4;
+  const int nvec = (int)((long long)H * elem / 16);
+  const int total = T * nvec;
+  if (total == 0) return hipSuccess;
+  if (y_dtype == 0) return launch_combine_t<true>(y, pair_row, w, shared, total, nvec, k, out, s);
+  return launch_combine_t<false>(y, pair_row, w, shared, total, nvec, k, out, s);
+}
+
+}  // namespace moe

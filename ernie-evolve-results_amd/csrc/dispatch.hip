@@ -1,0 +1,210 @@
+// Stage 3: expert offsets and the stable expert-major permutation.
+//
+// Replaces the scan half of offsets_kernel (K:2069-2086) and dispatch_body
+// (K:2109-2189).  The reference reserves positions with one global atomicAdd
+// per expert per block, so a row's place inside its expert segment depends on
+// which block got there first (K:2155-2158).  Here the order is fixed: pairs
+// are ranked by their flat index t*k + j, giving exactly
+// argsort(topk_ids.flatten(), stable) -- by expert, then ascending token.
+//
+// Three launches, all integer work over the T*k ids (1 MB at T=32768, k=8):
+//   1. pair_hist:   per block of 256 pairs, one 64-bit LDS bitmask word per
+//                   (expert, wave) marks which pairs chose the expert; the
+//                   popcounts are the block's expert histogram.
+//   2. block_scan:  one workgroup per expert scans its column of block
+//                   histograms (exclusive, in place) and writes its total.
+//   3. index:       each block rebuilds its bitmasks, scans the E totals into
+//                   offsets in LDS, and places every pair at
+//                   offsets[e] + (rows of e in earlier blocks) + (popcount of
+//                   earlier pairs of this block that chose e).
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int kMaskWords = kPairsPerBlock / 64;  // one word per wave
+
+__device__ __forceinline__ void build_masks(const int* __restrict__ ids, long long npairs, int E,
+                                            unsigned long long* mask, int& e_out) {
+  const int tid = threadIdx.x;
+  const long long p = (long long)blockIdx.x * kPairsPerBlock + tid;
+  int e = -1;
+  if (p < npairs) {
+    e = ids[p];
+    if (e < 0 || e >= E) e = -1;
+  }
+  if (e >= 0) atomicOr(&mask[e * kMaskWords + (tid >> 6)], 1ull << (tid & 63));
+  e_out = e;
+}
+
+__global__ __launch_bounds__(kPairsPerBlock) void pair_hist_kernel(
+    const int* __restrict__ ids, long long npairs, int E, int nblk, int* __restrict__ blockcnt) {
+  extern __shared__ unsigned long long mask[];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < E * kMaskWords; i += kPairsPerBlock) mask[i] = 0ull;
+  __syncthreads();
+  int e;
+  build_masks(ids, npairs, E, mask, e);
+  __syncthreads();
+  for (int x = tid; x < E; x += kPairsPerBlock) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < kMaskWords; ++w) c += __popcll(mask[x * kMaskWords + w]);
+    blockcnt[(long long)x * nblk + blockIdx.x] = c;
+  }
+}
+
+// Exclusive scan of 256 ints held one per thread; returns the exclusive prefix
+// and the block total.  Wave scans by __shfl_up, then a 4-entry carry.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* sh4, int& total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += n;
+  }
+  if (lane == 63) sh4[wave] = inc;
+  __syncthreads();
+  int carry = 0;
+  for (int w = 0; w < wave; ++w) carry += sh4[w];
+  total = sh4[0] + sh4[1] + sh4[2] + sh4[3];
+  __syncthreads();
+  return carry + inc - v;
+}
+
+constexpr int kScanPerThread = 4;
+
+__global__ __launch_bounds__(256) void block_scan_kernel(int* __restrict__ blockcnt, int nblk,
+                                                         int* __restrict__ totals) {
+  __shared__ int sh4[4];
+  int* col = blockcnt + (long long)blockIdx.x * nblk;
+  const int tid = threadIdx.x;
+  int carry = 0;
+  for (int base = 0; base < nblk; base += 256 * kScanPerThread) {
+    int v[kScanPerThread];
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < kScanPerThread; ++i) {
+      const int idx = base + tid * kScanPerThread + i;
+      v[i] = idx < nblk ? col[idx] : 0;
+      s += v[i];
+    }
+    int total;
+    int ex = block_exclusive_scan(s, sh4, total) + carry;
+#pragma unroll
+    for (int i = 0; i < kScanPerThread; ++i) {
+      const int idx = base + tid * kScanPerThread + i;
+      if (idx < nblk) col[idx] = ex;
+      ex += v[i];
+    }
+    carry += total;
+  }
+  if (tid == 0) totals[blockIdx.x] = carry;
+}
+
+// Exclusive scan of cnt[0..E) into offs[0..E] held in LDS (E <= 1024).
+__device__ __forceinline__ void lds_offsets(const int* __restrict__ cnt, int E, int* offs,
+                                            int* sh4) {
+  const int tid = threadIdx.x;
+  int v[4];
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid * 4 + i;
+    v[i] = idx < E ? cnt[idx] : 0;
+    s += v[i];
+  }
+  int total;
+  int ex = block_exclusive_scan(s, sh4, total);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid * 4 + i;
+    if (idx < E) offs[idx] = ex;
+    ex += v[i];
+  }
+  if (tid == 0) offs[E] = total;
+}
+
+__global__ __launch_bounds__(kPairsPerBlock) void dispatch_index_kernel(
+    const int* __restrict__ ids, long long npairs, int E, int k, int nblk,
+    const int* __restrict__ blockbase, const int* __restrict__ totals,
+    int* __restrict__ row_token, int* __restrict__ pair_row, int* __restrict__ offsets_out,
+    int* __restrict__ counts_out) {
+  extern __shared__ unsigned long long mask[];
+  int* offs = reinterpret_cast<int*>(mask + E * kMaskWords);
+  __shared__ int sh4[4];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < E * kMaskWords; i += kPairsPerBlock) mask[i] = 0ull;
+  lds_offsets(totals, E, offs, sh4);  // contains __syncthreads
+  int e;
+  build_masks(ids, npairs, E, mask, e);
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    for (int i = tid; i <= E; i += kPairsPerBlock) {
+      if (offsets_out) offsets_out[i] = offs[i];
+      if (counts_out && i < E) counts_out[i] = totals[i];
+    }
+  }
+  const long long p = (long long)blockIdx.x * kPairsPerBlock + tid;
+  if (p >= npairs) return;
+  if (e < 0) {
+    pair_row[p] = -1;
+    return;
+  }
+  const int wv = tid >> 6, bit = tid & 63;
+  const unsigned long long* me = mask + e * kMaskWords;
+  int rank = __popcll(me[wv] & ((1ull << bit) - 1ull));
+  for (int w = 0; w < wv; ++w) rank += __popcll(me[w]);
+  const int pos = offs[e] + blockbase[(long long)e * nblk + blockIdx.x] + rank;
+  pair_row[p] = pos;
+  row_token[pos] = (int)(p / k);
+}
+
+__global__ __launch_bounds__(256) void offsets_kernel(const int* __restrict__ counts, int E,
+                                                      int* __restrict__ offsets) {
+  __shared__ int offs[1025];
+  __shared__ int sh4[4];
+  lds_offsets(counts, E, offs, sh4);
+  __syncthreads();
+  for (int i = threadIdx.x; i <= E; i += 256) offsets[i] = offs[i];
+}
+
+hipError_t launch_offsets(const int32_t* counts, int E, int32_t* offsets, hipStream_t s) {
+  hipLaunchKernelGGL(offsets_kernel, dim3(1), dim3(256), 0, s, counts, E, offsets);
+  return hipGetLastError();
+}
+
+// blockcnt: [E, nblk] int32 workspace; totals: [E] int32 workspace.
+hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
+                                 int32_t* totals, int32_t* row_token, int32_t* pair_row,
+                                 int32_t* offsets, int32_t* counts, hipStream_t s) {
+  const long long npairs = (long long)T * k;
+  const int nblk = dispatch_blocks(npairs);
+  if (nblk == 0) {
+    // No pairs: offsets and counts are all zero.
+    hipLaunchKernelGGL(block_scan_kernel, dim3(E), dim3(256), 0, s, blockcnt, 0, totals);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    if (offsets) {
+      hipLaunchKernelGGL(offsets_kernel, dim3(1), dim3(256), 0, s, totals, E, offsets);
+      err = hipGetLastError();
+      if (err != hipSuccess) return err;
+    }
+    if (counts) return hipMemcpyAsync(counts, totals, sizeof(int) * E, hipMemcpyDeviceToDevice, s);
+    return hipSuccess;
+  }
+  const size_t shm_hist = sizeof(unsigned long long) * E * kMaskWords;
+  hipLaunchKernelGGL(pair_hist_kernel, dim3(nblk), dim3(kPairsPerBlock), shm_hist, s, ids,
+                     npairs, E, nblk, blockcnt);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(block_scan_kernel, dim3(E), dim3(256), 0, s, blockcnt, nblk, totals);
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const size_t shm_idx = shm_hist + sizeof(int) * (E + 1);
+  hipLaunchKernelGGL(dispatch_index_kernel, dim3(nblk), dim3(kPairsPerBlock), shm_idx, s, ids,
+                     npairs, E, k, nblk, blockcnt, totals, row_token, pair_row, offsets, counts);
+  return hipGetLastError();
+}
+
+}  // namespace moe

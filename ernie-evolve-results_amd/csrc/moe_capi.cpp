@@ -1,0 +1,254 @@
+// extern "C" entry points of libmoe_route.so (declared in include/moe_route.h).
+//
+// Every entry point validates its arguments on the host -- the role
+// TORCH_CHECK plays in the reference's run() (K:4088, K:4331-4338) -- and
+// only then enqueues kernels on the caller's stream.  Nothing here allocates
+// device memory or synchronises: scratch space is the caller's workspace
+// (the reference's per-call arena, K:4197-4268, becomes a caller-owned
+// buffer whose size moe_*_workspace_bytes reports).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/moe_route.h"
+#include "moe_common.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return MOE_OK;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    return fail(MOE_ERR_LAUNCH, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+  return ok();
+}
+
+bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Largest T*H / 8 (16-byte vectors per tensor) the 32-bit element loops take.
+constexpr long long kMaxVectors = (1ll << 31) - (1ll << 25);
+
+bool supported_e(int E) {
+  return E == 8 || E == 16 || E == 32 || E == 64 || E == 128 || E == 256;
+}
+
+int check_cfg(const moe_route_cfg* cfg, int E, int k) {
+  if (!cfg) return fail(MOE_ERR_NULL_POINTER, "cfg is NULL");
+  if (cfg->scoring < MOE_SCORING_SOFTMAX || cfg->scoring > MOE_SCORING_SOFTMAX_BIAS)
+    return fail(MOE_ERR_INVALID_ARG, "unknown scoring rule %d", cfg->scoring);
+  if (cfg->scoring == MOE_SCORING_SIGMOID_GROUP && cfg->n_group > 1) {
+    const int ng = cfg->n_group;
+    if (!pow2(ng) || E % ng != 0)
+      return fail(MOE_ERR_INVALID_ARG, "n_group=%d must be a power of two dividing E=%d", ng, E);
+    const int gs = E / ng;
+    const int V = E <= 64 ? 1 : E / 64;
+    if (gs < 2 || gs % V != 0)
+      return fail(MOE_ERR_UNSUPPORTED, "group size %d (E=%d, n_group=%d) below %d experts", gs,
+                  E, ng, V < 2 ? 2 : V);
+    if (cfg->topk_group < 1 || cfg->topk_group > ng)
+      return fail(MOE_ERR_INVALID_ARG, "topk_group=%d not in [1, n_group=%d]", cfg->topk_group,
+                  ng);
+    if ((long long)cfg->topk_group * gs < k)
+      return fail(MOE_ERR_INVALID_ARG, "topk_group*group_size=%d < k=%d", cfg->topk_group * gs,
+                  k);
+  } else if (cfg->n_group < 1) {
+    return fail(MOE_ERR_INVALID_ARG, "n_group=%d < 1", cfg->n_group);
+  }
+  return MOE_OK;
+}
+
+int check_topk_shape(int T, int E, int k) {
+  if (T < 0) return fail(MOE_ERR_INVALID_ARG, "T=%d < 0", T);
+  if (!supported_e(E))
+    return fail(MOE_ERR_UNSUPPORTED, "E=%d not in {8,16,32,64,128,256}", E);
+  if (k < 1 || k > 8 || k > E) return fail(MOE_ERR_INVALID_ARG, "k=%d not in [1, min(8,E)]", k);
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_version(void) { return MOE_ROUTE_VERSION; }
+
+const char* moe_last_error_string(void) { return g_err; }
+
+size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype) {
+  if (w_dtype != MOE_DTYPE_FP32 || T < 0 || H < 0 || E < 0) return 0;
+  return round256((size_t)2 * E * H * 2) + round256((size_t)T * 2 * E * 4);
+}
+
+int moe_router_gemm(const void* x, const void* w, int T, int H, int E, float* logits,
+                    void* stream) {
+  if (!x || !w || !logits) return fail(MOE_ERR_NULL_POINTER, "x, w and logits are required");
+  if (T < 0 || H <= 0) return fail(MOE_ERR_INVALID_ARG, "T=%d, H=%d", T, H);
+  if (H % 64 != 0) return fail(MOE_ERR_UNSUPPORTED, "H=%d is not a multiple of 64", H);
+  if (!supported_e(E)) return fail(MOE_ERR_UNSUPPORTED, "E=%d not in {8,...,256}", E);
+  if (!aligned16(x) || !aligned16(w)) return fail(MOE_ERR_ALIGNMENT, "x/w not 16-byte aligned");
+  if (T == 0) return ok();
+  return launched(moe::launch_router_gemm((const __bf16*)x, (const __bf16*)w, T, H, E, logits,
+                                          (hipStream_t)stream),
+                  "router_gemm");
+}
+
+int moe_topk(const float* logits, const float* bias, int T, int E, int k,
+             const moe_route_cfg* cfg, int32_t* topk_ids, float* topk_w, int32_t* counts,
+             void* stream) {
+  int rc = check_topk_shape(T, E, k);
+  if (rc) return rc;
+  if ((rc = check_cfg(cfg, E, k))) return rc;
+  if (T > 0 && (!logits || !topk_ids || !topk_w))
+    return fail(MOE_ERR_NULL_POINTER, "logits, topk_ids and topk_w are required");
+  if (logits && !aligned16(logits)) return fail(MOE_ERR_ALIGNMENT, "logits not 16-byte aligned");
+  return launched(moe::launch_topk(logits, 0, bias, T, E, k, cfg->scoring, cfg->renormalize,
+                                   cfg->n_group, cfg->topk_group, cfg->route_scale,
+                                   cfg->norm_min, nullptr, topk_ids, topk_w, counts,
+                                   (hipStream_t)stream),
+                  "topk");
+}
+
+int moe_route(const void* x, const void* w, int w_dtype, const float* bias, int T, int H, int E,
+              int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids, float* topk_w,
+              int32_t* counts, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_topk_shape(T, E, k);
+  if (rc) return rc;
+  if ((rc = check_cfg(cfg, E, k))) return rc;
+  if (w_dtype != MOE_DTYPE_BF16 && w_dtype != MOE_DTYPE_FP32)
+    return fail(MOE_ERR_UNSUPPORTED, "w_dtype=%d (BF16 or FP32 only)", w_dtype);
+  if (!x || !w || !logits || !topk_ids || !topk_w)
+    return fail(MOE_ERR_NULL_POINTER, "x, w, logits, topk_ids and topk_w are required");
+  if (H <= 0 || H % 64 != 0) return fail(MOE_ERR_UNSUPPORTED, "H=%d is not a positive multiple of 64", H);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(logits))
+    return fail(MOE_ERR_ALIGNMENT, "x, w and logits must be 16-byte aligned");
+  const size_t need = moe_route_workspace_bytes(T, H, E, w_dtype);
+  if (need > 0 && (!ws || ws_bytes < need))
+    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
+  if (need > 0 && !aligned16(ws)) return fail(MOE_ERR_ALIGNMENT, "workspace not 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  if (T == 0)
+    return launched(moe::launch_topk(nullptr, 0, bias, 0, E, k, cfg->scoring, cfg->renormalize,
+                                     cfg->n_group, cfg->topk_group, cfg->route_scale,
+                                     cfg->norm_min, nullptr, topk_ids, topk_w, counts, s),
+                    "topk");
+  if (w_dtype == MOE_DTYPE_BF16) {
+    rc = launched(moe::launch_router_gemm((const __bf16*)x, (const __bf16*)w, T, H, E, logits, s),
+                  "router_gemm");
+    if (rc) return rc;
+    return launched(moe::launch_topk(logits, 0, bias, T, E, k, cfg->scoring, cfg->renormalize,
+                                     cfg->n_group, cfg->topk_group, cfg->route_scale,
+                                     cfg->norm_min, nullptr, topk_ids, topk_w, counts, s),
+                    "topk");
+  }
+  // fp32 weights: hi/lo split, one GEMM against [2E,H], topk folds the halves.
+  __bf16* wpk = (__bf16*)ws;
+  float* dpk = (float*)((char*)ws + round256((size_t)2 * E * H * 2));
+  rc = launched(moe::launch_wsplit((const float*)w, wpk, E, H, s), "wsplit");
+  if (rc) return rc;
+  rc = launched(moe::launch_router_gemm((const __bf16*)x, wpk, T, H, 2 * E, dpk, s),
+                "router_gemm");
+  if (rc) return rc;
+  return launched(moe::launch_topk(dpk, 1, bias, T, E, k, cfg->scoring, cfg->renormalize,
+                                   cfg->n_group, cfg->topk_group, cfg->route_scale,
+                                   cfg->norm_min, logits, topk_ids, topk_w, counts, s),
+                  "topk");
+}
+
+int moe_offsets(const int32_t* counts, int E, int32_t* offsets, void* stream) {
+  if (!counts || !offsets) return fail(MOE_ERR_NULL_POINTER, "counts and offsets are required");
+  if (E < 1 || E > 1024) return fail(MOE_ERR_INVALID_ARG, "E=%d not in [1, 1024]", E);
+  return launched(moe::launch_offsets(counts, E, offsets, (hipStream_t)stream), "offsets");
+}
+
+size_t moe_permute_workspace_bytes(int T, int E, int k) {
+  if (T < 0 || E < 0 || k < 0) return 0;
+  const int nblk = moe::dispatch_blocks((long long)T * k);
+  return round256((size_t)E * nblk * 4) + round256((size_t)E * 4);
+}
+
+int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H, int E, int k,
+                int out_dtype, void* xg, float* scales, int32_t* row_token, int32_t* pair_row,
+                int32_t* offsets, int32_t* counts, void* ws, size_t ws_bytes, void* stream) {
+  if (T < 0 || H <= 0) return fail(MOE_ERR_INVALID_ARG, "T=%d, H=%d", T, H);
+  if (E < 1 || E > 1024) return fail(MOE_ERR_INVALID_ARG, "E=%d not in [1, 1024]", E);
+  if (k < 1 || k > 8) return fail(MOE_ERR_INVALID_ARG, "k=%d not in [1, 8]", k);
+  if (x_dtype != MOE_DTYPE_BF16 && x_dtype != MOE_DTYPE_FP32)
+    return fail(MOE_ERR_UNSUPPORTED, "x_dtype=%d (BF16 or FP32 only)", x_dtype);
+  const bool fp8 = out_dtype == MOE_DTYPE_FP8E4M3FN;
+  if (!fp8 && out_dtype != x_dtype)
+    return fail(MOE_ERR_UNSUPPORTED, "out_dtype=%d must equal x_dtype=%d or be FP8E4M3FN",
+                out_dtype, x_dtype);
+  if (fp8 && x_dtype != MOE_DTYPE_BF16)
+    return fail(MOE_ERR_UNSUPPORTED, "fp8 output needs bf16 x");
+  if (T > 0 && (!topk_ids || !row_token || !pair_row))
+    return fail(MOE_ERR_NULL_POINTER, "topk_ids, row_token and pair_row are required");
+  const int elem = x_dtype == MOE_DTYPE_BF16 ? 2 : 4;
+  if (xg) {
+    if (!x) return fail(MOE_ERR_NULL_POINTER, "x is required when xg is given");
+    if (fp8) {
+      if (H % 128 != 0) return fail(MOE_ERR_UNSUPPORTED, "fp8 permute needs H %% 128 == 0 (H=%d)", H);
+      if (!scales) return fail(MOE_ERR_NULL_POINTER, "fp8 permute needs scales");
+    } else if (((long long)H * elem) % 16 != 0) {
+      return fail(MOE_ERR_ALIGNMENT, "row of %d bytes is not a multiple of 16", H * elem);
+    }
+    if (!aligned16(x) || !aligned16(xg))
+      return fail(MOE_ERR_ALIGNMENT, "x and xg must be 16-byte aligned");
+    if ((long long)T * H * elem / 16 > kMaxVectors)
+      return fail(MOE_ERR_UNSUPPORTED, "T*H too large for one call (%lld vectors)",
+                  (long long)T * H * elem / 16);
+  }
+  const size_t need = moe_permute_workspace_bytes(T, E, k);
+  if (!ws || ws_bytes < need)
+    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
+  if (((long long)T * k) >= (1ll << 31))
+    return fail(MOE_ERR_UNSUPPORTED, "T*k=%lld exceeds int32 rows", (long long)T * k);
+  hipStream_t s = (hipStream_t)stream;
+  const int nblk = moe::dispatch_blocks((long long)T * k);
+  int32_t* blockcnt = (int32_t*)ws;
+  int32_t* totals = (int32_t*)((char*)ws + round256((size_t)E * nblk * 4));
+  int rc = launched(moe::launch_dispatch_index(topk_ids, T, E, k, blockcnt, totals, row_token,
+                                               pair_row, offsets, counts, s),
+                    "dispatch_index");
+  if (rc || !xg || T == 0) return rc;
+  if (fp8) return launched(moe::launch_gather_fp8(x, pair_row, T, H, k, xg, scales, s), "gather_fp8");
+  return launched(moe::launch_gather(x, elem, pair_row, T, H, k, xg, s), "gather");
+}
+
+int moe_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* topk_w,
+                const void* shared, int T, int H, int k, void* out, void* stream) {
+  if (T < 0 || H <= 0) return fail(MOE_ERR_INVALID_ARG, "T=%d, H=%d", T, H);
+  if (k < 1 || k > 8) return fail(MOE_ERR_INVALID_ARG, "k=%d not in [1, 8]", k);
+  if (y_dtype != MOE_DTYPE_BF16 && y_dtype != MOE_DTYPE_FP32)
+    return fail(MOE_ERR_UNSUPPORTED, "y_dtype=%d (BF16 or FP32 only)", y_dtype);
+  if (T == 0) return ok();
+  if (!y || !pair_row || !topk_w || !out)
+    return fail(MOE_ERR_NULL_POINTER, "y, pair_row, topk_w and out are required");
+  const int elem = y_dtype == MOE_DTYPE_BF16 ? 2 : 4;
+  if (((long long)H * elem) % 16 != 0)
+    return fail(MOE_ERR_ALIGNMENT, "row of %d bytes is not a multiple of 16", H * elem);
+  if (!aligned16(y) || !aligned16(out) || (shared && !aligned16(shared)))
+    return fail(MOE_ERR_ALIGNMENT, "y, out and shared must be 16-byte aligned");
+  if ((long long)T * H * elem / 16 > kMaxVectors)
+    return fail(MOE_ERR_UNSUPPORTED, "T*H too large for one call");
+  return launched(moe::launch_combine(y, y_dtype == MOE_DTYPE_BF16 ? 0 : 1, pair_row, topk_w,
+                                      shared, T, H, k, out, (hipStream_t)stream),
+                  "combine");
+}
+
+}  // extern "C"

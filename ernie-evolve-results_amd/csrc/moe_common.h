@@ -1,0 +1,66 @@
+// Shared types and launch helpers of libmoe_route (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// bf16 <-> fp32 without library help: bf16 is the top half of an fp32.
+__device__ __forceinline__ float bf16lo(unsigned int u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16hi(unsigned int u) { return __uint_as_float(u & 0xffff0000u); }
+
+// fp32 -> bf16 bits, round to nearest even (inputs here are finite).
+__device__ __forceinline__ unsigned int f2bf(float f) {
+  unsigned int u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ unsigned int pack_bf16x2(float lo, float hi) {
+  return f2bf(lo) | (f2bf(hi) << 16);
+}
+
+// Streaming (non-temporal) 16-byte global load / store: every byte of the
+// routed rows is touched once, so they should not displace reusable lines.
+__device__ __forceinline__ u32x4 ld_nt(const u32x4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st_nt(u32x4* p, u32x4 v) { __builtin_nontemporal_store(v, p); }
+
+}  // namespace moe
+
+// ---------------------------------------------------------------------------
+// Host-side launch wrappers, one per stage.  Each returns hipSuccess or the
+// runtime's error; argument validation happens in moe_capi.hip before them.
+// ---------------------------------------------------------------------------
+namespace moe {
+
+hipError_t launch_wsplit(const float* w, __bf16* wpk, int E, int H, hipStream_t s);
+hipError_t launch_router_gemm(const __bf16* x, const __bf16* w, int T, int H, int N,
+                              float* out, hipStream_t s);
+hipError_t launch_topk(const float* logits, int fold, const float* bias, int T, int E, int k,
+                       int scoring, int renorm, int n_group, int topk_group, float route_scale,
+                       float norm_min, float* logits_out, int32_t* ids, float* w,
+                       int32_t* counts, hipStream_t s);
+hipError_t launch_offsets(const int32_t* counts, int E, int32_t* offsets, hipStream_t s);
+hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
+                                 int32_t* totals, int32_t* row_token, int32_t* pair_row,
+                                 int32_t* offsets, int32_t* counts, hipStream_t s);
+hipError_t launch_gather(const void* x, int elem_bytes, const int32_t* pair_row, int T, int H,
+                         int k, void* xg, hipStream_t s);
+hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, int T, int H, int k,
+                             void* xg, float* scales, hipStream_t s);
+hipError_t launch_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* w,
+                          const void* shared, int T, int H, int k, void* out, hipStream_t s);
+
+// Number of pairs one dispatch block ranks (per-block expert bitmasks).
+constexpr int kPairsPerBlock = 256;
+inline int dispatch_blocks(long long npairs) {
+  return (int)((npairs + kPairsPerBlock - 1) / kPairsPerBlock);
+}
+
+}  // namespace moe

@@ -1,0 +1,351 @@
+"""moe_route: MI355X-native MoE route -> dispatch -> combine.
+
+Python host side of libmoe_route.so.  Mirrors the reference's operator
+interface: the whole-layer entry point ``run`` keeps the signature of
+``sol-execbench/029_moe_sparse_routing_and_dispatch/kernel.cu::run``
+(K:4067-4077, bound at K:5729-5735), and the stage functions expose the five
+stages it launches (K:4323-4431, K:5710-5718).
+
+PyTorch only provides device memory and the current HIP stream; every stage
+runs in the library's HIP kernels.  There is no CPU fallback: a missing
+library or a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+from .configs import (CONFIGS, SCORING_SIGMOID_GROUP, SCORING_SOFTMAX, SCORING_SOFTMAX_BIAS,
+                      MoeConfig, RouteCfg, make_inputs)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmoe_route.so")
+
+DTYPE_BF16, DTYPE_FP32, DTYPE_FP8E4M3FN = 0, 1, 2
+ERR_NAMES = {-1: "MOE_ERR_NULL_POINTER", -2: "MOE_ERR_INVALID_ARG", -3: "MOE_ERR_UNSUPPORTED",
+             -4: "MOE_ERR_WORKSPACE", -5: "MOE_ERR_LAUNCH", -6: "MOE_ERR_ALIGNMENT"}
+
+# Every extern "C" symbol of include/moe_route.h.
+EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
+           "moe_router_gemm", "moe_topk", "moe_route", "moe_offsets",
+           "moe_permute_workspace_bytes", "moe_permute", "moe_combine"]
+
+
+class MoeError(RuntimeError):
+    """A libmoe_route entry point returned an error code (the reference raises
+    RuntimeError from TORCH_CHECK, K:1771-1775)."""
+
+    def __init__(self, code, msg):
+        super().__init__("%s (%d): %s" % (ERR_NAMES.get(code, "MOE_ERR"), code, msg))
+        self.code = code
+
+
+class _Cfg(ctypes.Structure):
+    _fields_ = [("scoring", ctypes.c_int), ("renormalize", ctypes.c_int),
+                ("n_group", ctypes.c_int), ("topk_group", ctypes.c_int),
+                ("route_scale", ctypes.c_float), ("norm_min", ctypes.c_float)]
+
+
+_lib = None
+_P, _I, _Z, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
+
+
+def lib():
+    """Load libmoe_route.so (built by moe_route.build); raise if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("libmoe_route.so is not built (%s); run "
+                               "`python -m moe_route.build` or __graft_entry__.build()" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        L.moe_version.restype = _I
+        L.moe_version.argtypes = []
+        L.moe_last_error_string.restype = ctypes.c_char_p
+        L.moe_last_error_string.argtypes = []
+        L.moe_route_workspace_bytes.restype = _Z
+        L.moe_route_workspace_bytes.argtypes = [_I, _I, _I, _I]
+        L.moe_permute_workspace_bytes.restype = _Z
+        L.moe_permute_workspace_bytes.argtypes = [_I, _I, _I]
+        L.moe_router_gemm.restype = _I
+        L.moe_router_gemm.argtypes = [_P, _P, _I, _I, _I, _P, _P]
+        L.moe_topk.restype = _I
+        L.moe_topk.argtypes = [_P, _P, _I, _I, _I, ctypes.POINTER(_Cfg), _P, _P, _P, _P]
+        L.moe_route.restype = _I
+        L.moe_route.argtypes = [_P, _P, _I, _P, _I, _I, _I, _I, ctypes.POINTER(_Cfg), _P, _P, _P,
+                                _P, _P, _Z, _P]
+        L.moe_offsets.restype = _I
+        L.moe_offsets.argtypes = [_P, _I, _P, _P]
+        L.moe_permute.restype = _I
+        L.moe_permute.argtypes = [_P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _Z,
+                                  _P]
+        L.moe_combine.restype = _I
+        L.moe_combine.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise MoeError(rc, lib().moe_last_error_string().decode())
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _dev(t, name):
+    if not (isinstance(t, torch.Tensor) and t.is_cuda):
+        raise RuntimeError("%s must be a CUDA (HIP) tensor; libmoe_route has no CPU path" % name)
+    if not t.is_contiguous():
+        raise RuntimeError("%s must be contiguous" % name)
+    return t
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ccfg(cfg: RouteCfg):
+    return _Cfg(int(cfg.scoring), int(bool(cfg.renormalize)), int(cfg.n_group),
+                int(cfg.topk_group), float(cfg.route_scale), float(cfg.norm_min))
+
+
+def _dtype_code(dt):
+    if dt == torch.bfloat16:
+        return DTYPE_BF16
+    if dt == torch.float32:
+        return DTYPE_FP32
+    raise RuntimeError("unsupported dtype %s" % dt)
+
+
+# ---------------------------------------------------------------------------
+# stage functions
+# ---------------------------------------------------------------------------
+def router_gemm(x, w):
+    """logits[T,E] fp32 = x[T,H] bf16 . w[E,H]^T bf16 (K:4327-4339)."""
+    _dev(x, "x"), _dev(w, "w")
+    T, H = x.shape
+    E = w.shape[0]
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise RuntimeError("router_gemm takes bf16 x and w")
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
+    _check(lib().moe_router_gemm(_ptr(x), _ptr(w), T, H, E, _ptr(logits), _stream(x)))
+    return logits
+
+
+def topk(logits, bias, k, cfg: RouteCfg):
+    """Scoring + top-k + histogram on fp32 logits (K:1829-1920).
+    Returns (topk_ids int32 [T,k], topk_w fp32 [T,k], counts int32 [E])."""
+    _dev(logits, "logits")
+    T, E = logits.shape
+    if bias is not None:
+        _dev(bias, "bias")
+    ids = torch.empty(T, k, dtype=torch.int32, device=logits.device)
+    wts = torch.empty(T, k, dtype=torch.float32, device=logits.device)
+    counts = torch.empty(E, dtype=torch.int32, device=logits.device)
+    c = _ccfg(cfg)
+    _check(lib().moe_topk(_ptr(logits), _ptr(bias), T, E, k, ctypes.byref(c), _ptr(ids),
+                          _ptr(wts), _ptr(counts), _stream(logits)))
+    return ids, wts, counts
+
+
+def route(x, w, bias, k, cfg: RouteCfg):
+    """Router GEMM + scoring + top-k + histogram.  w bf16 [E,H], or fp32 [E,H]
+    (hi/lo split on the device, K:1786-1824).
+    Returns (logits fp32 [T,E], topk_ids, topk_w, counts)."""
+    _dev(x, "x"), _dev(w, "w")
+    T, H = x.shape
+    E = w.shape[0]
+    wd = _dtype_code(w.dtype)
+    if bias is not None:
+        _dev(bias, "bias")
+    dev = x.device
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+    wts = torch.empty(T, k, dtype=torch.float32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    L = lib()
+    nws = L.moe_route_workspace_bytes(T, H, E, wd)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+    c = _ccfg(cfg)
+    _check(L.moe_route(_ptr(x), _ptr(w), wd, _ptr(bias), T, H, E, k, ctypes.byref(c),
+                       _ptr(logits), _ptr(ids), _ptr(wts), _ptr(counts), _ptr(ws), nws,
+                       _stream(x)))
+    return logits, ids, wts, counts
+
+
+def offsets(counts):
+    """Exclusive offsets [E+1] of counts [E] (K:2069-2086)."""
+    _dev(counts, "counts")
+    E = counts.shape[0]
+    out = torch.empty(E + 1, dtype=torch.int32, device=counts.device)
+    _check(lib().moe_offsets(_ptr(counts), E, _ptr(out), _stream(counts)))
+    return out
+
+
+def permute(x, topk_ids, E, fp8=False, index_only=False):
+    """Stable expert-major permutation + gather (K:1922-2238).
+
+    Returns dict(xg, scales, row_token, pair_row, offsets, counts); xg is
+    x.dtype rows (or uint8 e4m3fn bytes when fp8) in expert-contiguous order."""
+    _dev(x, "x"), _dev(topk_ids, "topk_ids")
+    T, H = x.shape
+    k = topk_ids.shape[1]
+    dev = x.device
+    xd = _dtype_code(x.dtype)
+    od = DTYPE_FP8E4M3FN if fp8 else xd
+    ns = T * k
+    xg = scales = None
+    if not index_only:
+        if fp8:
+            xg = torch.empty(ns, H, dtype=torch.uint8, device=dev)
+            scales = torch.empty(ns, H // 128, dtype=torch.float32, device=dev)
+        else:
+            xg = torch.empty(ns, H, dtype=x.dtype, device=dev)
+    row_token = torch.empty(ns, dtype=torch.int32, device=dev)
+    pair_row = torch.empty(ns, dtype=torch.int32, device=dev)
+    offs = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    L = lib()
+    nws = L.moe_permute_workspace_bytes(T, E, k)
+    ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
+    _check(L.moe_permute(_ptr(x), xd, _ptr(topk_ids), T, H, E, k, od, _ptr(xg), _ptr(scales),
+                         _ptr(row_token), _ptr(pair_row), _ptr(offs), _ptr(counts), _ptr(ws),
+                         nws, _stream(x)))
+    return dict(xg=xg, scales=scales, row_token=row_token, pair_row=pair_row, offsets=offs,
+                counts=counts)
+
+
+def combine(y, pair_row, topk_w, shared=None, out=None):
+    """out[t] = shared[t] + sum_j w[t,j] * y[pair_row[t,j]], fp32 accumulate
+    (K:2365-2428)."""
+    _dev(y, "y"), _dev(pair_row, "pair_row"), _dev(topk_w, "topk_w")
+    T, k = topk_w.shape
+    H = y.shape[1]
+    if shared is not None:
+        _dev(shared, "shared")
+    if out is None:
+        out = torch.empty(T, H, dtype=y.dtype, device=y.device)
+    _check(lib().moe_combine(_ptr(y), _dtype_code(y.dtype), _ptr(pair_row), _ptr(topk_w),
+                             _ptr(shared), T, H, k, _ptr(out), _stream(y)))
+    return out
+
+
+def route_dispatch_combine(x, w, bias, y, k, cfg: RouteCfg, fp8=False):
+    """The whole path for one batch: route, permute (bf16 or fp8), combine y."""
+    logits, ids, wts, counts = route(x, w, bias, k, cfg)
+    p = permute(x, ids, w.shape[0], fp8=fp8)
+    out = combine(y, p["pair_row"], wts) if y is not None else None
+    p.update(logits=logits, topk_ids=ids, topk_w=wts, route_counts=counts, out=out)
+    return p
+
+
+# ---------------------------------------------------------------------------
+# the reference entry point
+# ---------------------------------------------------------------------------
+REF_NE, REF_TOPK = 64, 8  # K:1582-1583
+
+
+def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, expert_up_proj,
+        expert_down_proj, shared_gate_proj, shared_up_proj, shared_down_proj, norm_min):
+    """Drop-in for the reference's run() (K:4067-4077): returns
+    (out [B,S,H] bf16, router_logits [T,64] fp32).
+
+    Routing (fp32 gate_weight hi/lo split, softmax + post-softmax bias, top-8,
+    w = c / max(sum c, norm_min)), dispatch and combine run in libmoe_route.
+    The expert SwiGLU MLPs, which the reference runs as CUTLASS grouped GEMMs,
+    are plain torch matmuls over each expert's contiguous row range here."""
+    B, S, H = hidden_states.shape
+    T = B * S
+    x = hidden_states.reshape(T, H)
+    _dev(x, "hidden_states")
+    E = gate_weight.shape[0]
+    cfg = RouteCfg(SCORING_SOFTMAX_BIAS, True, 1, 1, 1.0, float(norm_min))
+    logits, ids, wts, _ = route(x, gate_weight.float().contiguous(),
+                                e_score_correction_bias.float().contiguous(), REF_TOPK, cfg)
+    p = permute(x, ids, E)
+    offs = p["offsets"].cpu().tolist()
+    xg = p["xg"]
+    y = torch.empty_like(xg)
+    silu = torch.nn.functional.silu
+    for e in range(E):
+        a, b = offs[e], offs[e + 1]
+        if a == b:
+            continue
+        xe = xg[a:b]
+        h = silu(xe @ expert_gate_proj[e].t()) * (xe @ expert_up_proj[e].t())
+        y[a:b] = h @ expert_down_proj[e].t()
+    sh = (silu(x @ shared_gate_proj.t()) * (x @ shared_up_proj.t())) @ shared_down_proj.t()
+    out = combine(y, p["pair_row"], wts, shared=sh.contiguous())
+    return out.view(B, S, H), logits
+
+
+# ---------------------------------------------------------------------------
+# preallocated plan: one batch shape, every buffer allocated once
+# ---------------------------------------------------------------------------
+class MoePlan:
+    """All outputs and workspaces of one (T, H, E, k) batch shape, allocated
+    once (the reference's per-call arena, K:4197-4268, hoisted out of the
+    call).  ``route`` / ``permute`` / ``combine`` / ``step`` then only enqueue
+    kernels on the current stream through the C ABI."""
+
+    def __init__(self, T, H, E, k, cfg: RouteCfg, device, fp8=False, w_dtype=torch.bfloat16,
+                 x_dtype=torch.bfloat16):
+        self.T, self.H, self.E, self.k, self.fp8 = T, H, E, k, fp8
+        self.cfg = _ccfg(cfg)
+        self.wd = _dtype_code(w_dtype)
+        self.xd = _dtype_code(x_dtype)
+        dev = torch.device(device)
+        ns = T * k
+        L = lib()
+        self.logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+        self.topk_ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+        self.topk_w = torch.empty(T, k, dtype=torch.float32, device=dev)
+        self.route_counts = torch.empty(E, dtype=torch.int32, device=dev)
+        self.row_token = torch.empty(ns, dtype=torch.int32, device=dev)
+        self.pair_row = torch.empty(ns, dtype=torch.int32, device=dev)
+        self.offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        self.counts = torch.empty(E, dtype=torch.int32, device=dev)
+        if fp8:
+            self.xg = torch.empty(ns, H, dtype=torch.uint8, device=dev)
+            self.scales = torch.empty(ns, H // 128, dtype=torch.float32, device=dev)
+        else:
+            self.xg = torch.empty(ns, H, dtype=x_dtype, device=dev)
+            self.scales = None
+        self.out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        self.nws_route = L.moe_route_workspace_bytes(T, H, E, self.wd)
+        self.ws_route = torch.empty(max(self.nws_route, 256), dtype=torch.uint8, device=dev)
+        self.nws_perm = L.moe_permute_workspace_bytes(T, E, k)
+        self.ws_perm = torch.empty(max(self.nws_perm, 256), dtype=torch.uint8, device=dev)
+
+    def route(self, x, w, bias):
+        _check(lib().moe_route(_ptr(x), _ptr(w), self.wd, _ptr(bias), self.T, self.H, self.E,
+                               self.k, ctypes.byref(self.cfg), _ptr(self.logits),
+                               _ptr(self.topk_ids), _ptr(self.topk_w), _ptr(self.route_counts),
+                               _ptr(self.ws_route), self.nws_route, _stream(x)))
+
+    def router_gemm(self, x, w):
+        _check(lib().moe_router_gemm(_ptr(x), _ptr(w), self.T, self.H, self.E, _ptr(self.logits),
+                                     _stream(x)))
+
+    def permute(self, x):
+        od = DTYPE_FP8E4M3FN if self.fp8 else self.xd
+        _check(lib().moe_permute(_ptr(x), self.xd, _ptr(self.topk_ids), self.T, self.H, self.E,
+                                 self.k, od, _ptr(self.xg), _ptr(self.scales),
+                                 _ptr(self.row_token), _ptr(self.pair_row), _ptr(self.offsets),
+                                 _ptr(self.counts), _ptr(self.ws_perm), self.nws_perm,
+                                 _stream(x)))
+
+    def combine(self, y, shared=None):
+        _check(lib().moe_combine(_ptr(y), _dtype_code(y.dtype), _ptr(self.pair_row),
+                                 _ptr(self.topk_w), _ptr(shared), self.T, self.H, self.k,
+                                 _ptr(self.out), _stream(y)))
+
+    def step(self, x, w, bias, y):
+        """route -> permute -> combine for one batch."""
+        self.route(x, w, bias)
+        self.permute(x)
+        self.combine(y)
+        return self.out

@@ -1,0 +1,143 @@
+/*
+ * moe_route.h -- C ABI of libmoe_route.so, the MI355X (gfx950) MoE
+ * route -> dispatch -> combine path.
+ *
+ * Reference: sol-execbench/029_moe_sparse_routing_and_dispatch/kernel.cu
+ * (abbreviated K).  The reference exposes the path as one PyTorch extension
+ * function, run() (K:4067-4077, bound at K:5729-5735), whose body launches the
+ * stage kernels listed beside each entry point below.  This library exposes
+ * the same stages as plain C functions over raw device pointers so that any
+ * host (ctypes, cgo, JNI, N-API, C++) can bind them.
+ *
+ * Conventions (all entry points):
+ *   - Pointers are device pointers (HBM) unless stated; tensors are dense and
+ *     row-major.  bf16 is IEEE bfloat16, fp8 is OCP float8 e4m3fn.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Every call only
+ *     enqueues work on that stream: no host synchronisation, no allocation, no
+ *     events (as the reference, K:57-58, K:4079).
+ *   - Return 0 on success, a negative MOE_ERR_* code otherwise; the message
+ *     is in moe_last_error_string() (thread-local).  Arguments are validated
+ *     on the host before anything is launched, so every error path is
+ *     testable without a GPU.
+ *   - Index outputs are int32.  A pair is (token t, slot j), flat index
+ *     t*k + j.  A row is a position in the expert-contiguous buffer.
+ */
+#ifndef MOE_ROUTE_H_
+#define MOE_ROUTE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_ROUTE_VERSION 1
+
+/* error codes */
+#define MOE_OK 0
+#define MOE_ERR_NULL_POINTER -1   /* a required pointer is NULL */
+#define MOE_ERR_INVALID_ARG -2    /* a size or configuration value is out of range */
+#define MOE_ERR_UNSUPPORTED -3    /* a valid combination this build has no kernel for */
+#define MOE_ERR_WORKSPACE -4      /* workspace missing or smaller than required */
+#define MOE_ERR_LAUNCH -5         /* the HIP runtime refused a launch */
+#define MOE_ERR_ALIGNMENT -6      /* a pointer or row size breaks 16-byte alignment */
+
+/* element types */
+#define MOE_DTYPE_BF16 0
+#define MOE_DTYPE_FP32 1
+#define MOE_DTYPE_FP8E4M3FN 2
+
+/* scoring rules (moe_route_cfg.scoring) */
+#define MOE_SCORING_SOFTMAX 0       /* top-k of logit(+bias); softmax weights (Mixtral, Qwen3) */
+#define MOE_SCORING_SIGMOID_GROUP 1 /* sigmoid; +bias for selection; group-limited (DeepSeek-V3) */
+#define MOE_SCORING_SOFTMAX_BIAS 2  /* softmax, +bias after softmax, / max(sum, norm_min): K:1857-1909 */
+
+/* Routing configuration.  The reference hard-wires softmax + post-softmax
+ * bias with NE=64, TOPK=8 (K:1582-1583, K:1857-1909); this struct carries the
+ * generalisation the benchmark configurations need. */
+typedef struct moe_route_cfg {
+  int scoring;       /* MOE_SCORING_* */
+  int renormalize;   /* 1: selected weights are renormalised to sum 1 (before route_scale) */
+  int n_group;       /* SIGMOID_GROUP: number of expert groups (1 = no group limit) */
+  int topk_group;    /* SIGMOID_GROUP: groups kept per token */
+  float route_scale; /* weights are multiplied by this (DeepSeek-V3: 2.5) */
+  float norm_min;    /* SOFTMAX_BIAS: denominator floor, the reference's norm_min (K:1909) */
+} moe_route_cfg;
+
+/* Library version (MOE_ROUTE_VERSION). */
+int moe_version(void);
+
+/* Message of the last error on the calling thread ("" if none).
+ * Replaces TORCH_CHECK's exception text (K:1771-1775, K:4088). */
+const char* moe_last_error_string(void);
+
+/* Workspace bytes moe_route needs.  w_dtype FP32 adds the hi/lo split weight
+ * [2E,H] bf16 and the packed logits [T,2E] fp32 (K:4197-4268 arena). */
+size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype);
+
+/* Stage 1: router GEMM, logits[T,E] fp32 = x[T,H] bf16 . w[E,H]^T bf16, fp32
+ * accumulate on MFMA.  Replaces the cublasGemmEx call K:4327-4339.
+ * Needs H % 64 == 0 and E in {8,16,32,64,128,256}. */
+int moe_router_gemm(const void* x, const void* w, int T, int H, int E, float* logits,
+                    void* stream);
+
+/* Stage 2 (+ histogram): scoring + top-k on fp32 logits.  Replaces
+ * topk_kernel K:1829-1920 (selection, weights, LDS histogram + global flush).
+ * bias: [E] fp32 or NULL.  Outputs topk_ids [T,k], topk_w [T,k], counts [E]
+ * (counts may be NULL).  Slots are ordered by descending selection score,
+ * ties to the lower expert index (K:1886).  1 <= k <= 8. */
+int moe_topk(const float* logits, const float* bias, int T, int E, int k,
+             const moe_route_cfg* cfg, int32_t* topk_ids, float* topk_w, int32_t* counts,
+             void* stream);
+
+/* Stages 1+2: router GEMM + scoring + top-k + histogram (run() K:4323-4354).
+ * w_dtype BF16: w is [E,H] bf16.  w_dtype FP32: w is [E,H] fp32 and is split
+ * into bf16 hi/lo on the device (wsplit_kernel K:1786-1824) so the bf16 GEMM
+ * yields fp32-accurate logits.  logits [T,E] fp32 (the reference's
+ * router_logits output), counts may be NULL. */
+int moe_route(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
+              int E, int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids,
+              float* topk_w, int32_t* counts, void* ws, size_t ws_bytes, void* stream);
+
+/* Exclusive prefix sum of counts[E] into offsets[E+1] (offsets[E] = total).
+ * offsets + 1 is the reference's inclusive group-end array offs
+ * (offsets_kernel scan K:2069-2086; moe_gemm.h:66-69).  E <= 1024. */
+int moe_offsets(const int32_t* counts, int E, int32_t* offsets, void* stream);
+
+/* Workspace bytes moe_permute needs (per-block expert histograms). */
+size_t moe_permute_workspace_bytes(int T, int E, int k);
+
+/* Stages 3+4: stable expert-major permutation and row gather.  Replaces
+ * offsets_kernel (scan part) + dispatch_kernel + gather_kernel
+ * (K:1922-2238).  Pairs are placed in the order argsort(topk_ids.flatten(),
+ * stable): by expert, then ascending token -- deterministic, unlike the
+ * reference's atomic order (K:2155-2158).
+ *   x        [T,H] of x_dtype (BF16 or FP32)
+ *   out_dtype == x_dtype: xg[T*k,H] rows are copies of x rows;
+ *   out_dtype FP8E4M3FN (x BF16 only): xg[T*k,H] bytes, scales[T*k,H/128] fp32,
+ *     q = e4m3fn(clamp(x / s, +-448)), s = max(amax over 128, 1e-10) / 448.
+ *   row_token[T*k]: token of each row (the reference's tok, K:2179)
+ *   pair_row[T*k] : row of each pair  (the reference's inv, K:2178)
+ *   offsets[E+1]  : exclusive expert offsets (may be NULL)
+ *   counts[E]     : per-expert row counts (may be NULL)
+ * xg may be NULL (index work only).  An id outside [0,E) gets pair_row -1 and
+ * no row.  Needs H*elem % 16 == 0 (FP8: H % 128 == 0). */
+int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H, int E,
+                int k, int out_dtype, void* xg, float* scales, int32_t* row_token,
+                int32_t* pair_row, int32_t* offsets, int32_t* counts, void* ws,
+                size_t ws_bytes, void* stream);
+
+/* Stage 5: weighted combine.  Replaces combine_kernel K:2365-2428:
+ *   out[t] = cast(shared[t] + sum_j topk_w[t,j] * y[pair_row[t,j]])
+ * accumulated in fp32 in slot order.  y [R,H] and out [T,H] of y_dtype (BF16
+ * or FP32); shared [T,H] of y_dtype or NULL; pairs with pair_row < 0 are
+ * skipped. */
+int moe_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* topk_w,
+                const void* shared, int T, int H, int k, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_ROUTE_H_ */

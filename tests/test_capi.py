@@ -1,0 +1,128 @@
+"""libmoe_route.so: loads, exports every declared symbol, and rejects bad
+arguments with the documented error codes -- all without a GPU (validation
+runs on the host before any launch)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import moe_route as M
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FAKE = ctypes.c_void_p(0x10000)  # never dereferenced: every call below fails validation
+
+
+def header_functions():
+    text = open(os.path.join(REPO, "include", "moe_route.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(moe_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    L = M.lib()
+    names = header_functions()
+    assert len(names) >= 10
+    assert sorted(M.EXPORTS) == names
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_version_and_empty_error():
+    assert M.lib().moe_version() == 1
+    assert M.lib().moe_last_error_string() == b""
+
+
+def cfg(**kw):
+    c = M._Cfg(0, 1, 1, 1, 1.0, 0.0)
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+def err(rc, code, fragment=None):
+    assert rc == code
+    msg = M.lib().moe_last_error_string().decode()
+    if fragment:
+        assert fragment in msg, msg
+
+
+def test_route_validation():
+    L = M.lib()
+    c = cfg()
+    args = lambda T=16, H=128, E=8, k=2, wd=0, x=FAKE: (x, FAKE, wd, None, T, H, E, k,
+                                                        ctypes.byref(c), FAKE, FAKE, FAKE, None,
+                                                        None, 0, None)
+    err(L.moe_route(*args(E=12)), -3, "E=12")
+    err(L.moe_route(*args(k=0)), -2, "k=0")
+    err(L.moe_route(*args(k=9, E=16)), -2)
+    err(L.moe_route(*args(H=100)), -3, "multiple of 64")
+    err(L.moe_route(*args(wd=2)), -3, "w_dtype")
+    err(L.moe_route(*args(x=None)), -1)
+    err(L.moe_route(*args(wd=1)), -4, "workspace")
+    err(L.moe_route(*args(x=ctypes.c_void_p(0x10008))), -6)
+    err(L.moe_route(*args(T=-1)), -2)
+
+
+def test_group_cfg_validation():
+    L = M.lib()
+    def topk(c, E=256, k=8):
+        return L.moe_topk(FAKE, None, 4, E, k, ctypes.byref(c), FAKE, FAKE, None, None)
+    err(topk(cfg(scoring=7)), -2, "scoring")
+    err(topk(cfg(scoring=1, n_group=6, topk_group=2)), -2, "power of two")
+    err(topk(cfg(scoring=1, n_group=8, topk_group=9)), -2, "topk_group")
+    err(topk(cfg(scoring=1, n_group=128, topk_group=4)), -3, "group size")
+    err(topk(cfg(scoring=1, n_group=64, topk_group=1), E=64, k=2), -3, "group size")
+    err(topk(cfg(scoring=1, n_group=32, topk_group=1), E=256, k=16), -2)
+    err(L.moe_topk(FAKE, None, 4, 256, 8, None, FAKE, FAKE, None, None), -1)
+
+
+def test_permute_and_combine_validation():
+    L = M.lib()
+    base = dict(x=FAKE, xd=0, ids=FAKE, T=8, H=256, E=16, k=2, od=0, xg=FAKE, sc=None,
+                rt=FAKE, pr=FAKE, ws=FAKE, nws=1 << 20)
+    def perm(**kw):
+        a = dict(base, **kw)
+        return L.moe_permute(a["x"], a["xd"], a["ids"], a["T"], a["H"], a["E"], a["k"], a["od"],
+                             a["xg"], a["sc"], a["rt"], a["pr"], None, None, a["ws"], a["nws"],
+                             None)
+    err(perm(od=1), -3, "out_dtype")
+    err(perm(od=2), -1, "scales")
+    err(perm(od=2, sc=FAKE, H=192), -3, "128")
+    err(perm(od=2, sc=FAKE, xd=1), -3)
+    err(perm(H=4), -6)
+    err(perm(E=0), -2)
+    err(perm(k=9), -2)
+    err(perm(nws=16), -4)
+    err(perm(rt=None), -1)
+    err(L.moe_combine(FAKE, 5, FAKE, FAKE, None, 4, 64, 2, FAKE, None), -3)
+    err(L.moe_combine(FAKE, 0, FAKE, FAKE, None, 4, 4, 2, FAKE, None), -6)
+    err(L.moe_combine(None, 0, FAKE, FAKE, None, 4, 64, 2, FAKE, None), -1)
+    err(L.moe_combine(FAKE, 0, FAKE, FAKE, None, 4, 64, 0, FAKE, None), -2)
+    assert L.moe_combine(None, 0, None, None, None, 0, 64, 2, None, None) == 0
+    err(L.moe_offsets(FAKE, 2000, FAKE, None), -2)
+    err(L.moe_router_gemm(FAKE, FAKE, 4, 96, 8, FAKE, None), -3)
+
+
+def test_workspace_sizes():
+    L = M.lib()
+    assert L.moe_route_workspace_bytes(100, 128, 8, 0) == 0
+    # fp32 weights: [2E,H] bf16 split + [T,2E] fp32 logits, each 256-aligned
+    assert L.moe_route_workspace_bytes(100, 128, 8, 1) == 4096 + 6400
+    # T*k = 32768*8 pairs -> 1024 blocks of 256; [E, nblk] + [E] int32
+    assert L.moe_permute_workspace_bytes(32768, 256, 8) == 256 * 1024 * 4 + 1024
+
+
+def test_python_layer_refuses_cpu_tensors():
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        M.router_gemm(x, x)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        M.permute(x, torch.zeros(4, 2, dtype=torch.int32), 8)
+
+
+def test_missing_library_raises(monkeypatch):
+    monkeypatch.setattr(M, "_lib", None)
+    monkeypatch.setattr(M, "LIB_PATH", "/nonexistent/libmoe_route.so")
+    with pytest.raises(RuntimeError, match="not built"):
+        M.lib()
