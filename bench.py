@@ -81,7 +81,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C4")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=8192)
+    ap.add_argument("--cpu-tokens", type=int, default=16384)
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run one plain 1 GiB device copy (untimed), the known-size "
+                         "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this path runs on one GPU only (no sharding, no collectives); "
@@ -97,6 +100,12 @@ def main():
     for _ in range(args.warmup):
         plan.step(x, w, bias, y)
     torch.cuda.synchronize()
+    if args.copy_calib:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     # ---- timed region: exactly K steps, whole path, inputs resident in HBM
     t0 = time.perf_counter()

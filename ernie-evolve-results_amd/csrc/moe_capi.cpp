@@ -58,10 +58,10 @@ int check_cfg(const moe_route_cfg* cfg, int E, int k) {
     if (!pow2(ng) || E % ng != 0)
       return fail(MOE_ERR_INVALID_ARG, "n_group=%d must be a power of two dividing E=%d", ng, E);
     const int gs = E / ng;
-    const int V = E <= 64 ? 1 : E / 64;
-    if (gs < 2 || gs % V != 0)
+    const int V = moe::topk_lane_width(E, cfg->scoring, ng);
+    if (gs < 2 || E / V > 64)
       return fail(MOE_ERR_UNSUPPORTED, "group size %d (E=%d, n_group=%d) below %d experts", gs,
-                  E, ng, V < 2 ? 2 : V);
+                  E, ng, gs < 2 ? 2 : E / 64);
     if (cfg->topk_group < 1 || cfg->topk_group > ng)
       return fail(MOE_ERR_INVALID_ARG, "topk_group=%d not in [1, n_group=%d]", cfg->topk_group,
                   ng);
@@ -90,9 +90,21 @@ int moe_version(void) { return MOE_ROUTE_VERSION; }
 
 const char* moe_last_error_string(void) { return g_err; }
 
+// Partial-logit blocks per row the route path produces: 2 for an fp32 weight
+// (hi/lo halves) times the GEMM's K partitions.
+static int route_parts(int T, int H, int E, int w_dtype) {
+  const int N = w_dtype == MOE_DTYPE_FP32 ? 2 * E : E;
+  return (N / E) * moe::router_gemm_ksplit(T, H, N);
+}
+
 size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype) {
-  if (w_dtype != MOE_DTYPE_FP32 || T < 0 || H < 0 || E < 0) return 0;
-  return round256((size_t)2 * E * H * 2) + round256((size_t)T * 2 * E * 4);
+  if (T < 0 || H < 0 || E <= 0) return 0;
+  if (w_dtype != MOE_DTYPE_BF16 && w_dtype != MOE_DTYPE_FP32) return 0;
+  const int parts = route_parts(T, H, E, w_dtype);
+  size_t b = 0;
+  if (w_dtype == MOE_DTYPE_FP32) b += round256((size_t)2 * E * H * 2);
+  if (parts > 1) b += round256((size_t)T * parts * E * 4);
+  return b;
 }
 
 int moe_router_gemm(const void* x, const void* w, int T, int H, int E, float* logits,
@@ -103,7 +115,7 @@ int moe_router_gemm(const void* x, const void* w, int T, int H, int E, float* lo
   if (!supported_e(E)) return fail(MOE_ERR_UNSUPPORTED, "E=%d not in {8,...,256}", E);
   if (!aligned16(x) || !aligned16(w)) return fail(MOE_ERR_ALIGNMENT, "x/w not 16-byte aligned");
   if (T == 0) return ok();
-  return launched(moe::launch_router_gemm((const __bf16*)x, (const __bf16*)w, T, H, E, logits,
+  return launched(moe::launch_router_gemm((const __bf16*)x, (const __bf16*)w, T, H, E, 1, logits,
                                           (hipStream_t)stream),
                   "router_gemm");
 }
@@ -117,7 +129,7 @@ int moe_topk(const float* logits, const float* bias, int T, int E, int k,
   if (T > 0 && (!logits || !topk_ids || !topk_w))
     return fail(MOE_ERR_NULL_POINTER, "logits, topk_ids and topk_w are required");
   if (logits && !aligned16(logits)) return fail(MOE_ERR_ALIGNMENT, "logits not 16-byte aligned");
-  return launched(moe::launch_topk(logits, 0, bias, T, E, k, cfg->scoring, cfg->renormalize,
+  return launched(moe::launch_topk(logits, 1, bias, T, E, k, cfg->scoring, cfg->renormalize,
                                    cfg->n_group, cfg->topk_group, cfg->route_scale,
                                    cfg->norm_min, nullptr, topk_ids, topk_w, counts,
                                    (hipStream_t)stream),
@@ -143,30 +155,33 @@ int moe_route(const void* x, const void* w, int w_dtype, const float* bias, int 
   if (need > 0 && !aligned16(ws)) return fail(MOE_ERR_ALIGNMENT, "workspace not 16-byte aligned");
   hipStream_t s = (hipStream_t)stream;
   if (T == 0)
-    return launched(moe::launch_topk(nullptr, 0, bias, 0, E, k, cfg->scoring, cfg->renormalize,
+    return launched(moe::launch_topk(nullptr, 1, bias, 0, E, k, cfg->scoring, cfg->renormalize,
                                      cfg->n_group, cfg->topk_group, cfg->route_scale,
                                      cfg->norm_min, nullptr, topk_ids, topk_w, counts, s),
                     "topk");
-  if (w_dtype == MOE_DTYPE_BF16) {
-    rc = launched(moe::launch_router_gemm((const __bf16*)x, (const __bf16*)w, T, H, E, logits, s),
-                  "router_gemm");
+  const int N = w_dtype == MOE_DTYPE_FP32 ? 2 * E : E;
+  const int ksplit = moe::router_gemm_ksplit(T, H, N);
+  const int parts = (N / E) * ksplit;
+  const __bf16* wb = (const __bf16*)w;
+  char* wsp = (char*)ws;
+  if (w_dtype == MOE_DTYPE_FP32) {
+    // fp32 weights: hi/lo bf16 split (K:1786-1824), one GEMM against [2E,H]
+    __bf16* wpk = (__bf16*)wsp;
+    wsp += round256((size_t)2 * E * H * 2);
+    rc = launched(moe::launch_wsplit((const float*)w, wpk, E, H, s), "wsplit");
     if (rc) return rc;
-    return launched(moe::launch_topk(logits, 0, bias, T, E, k, cfg->scoring, cfg->renormalize,
-                                     cfg->n_group, cfg->topk_group, cfg->route_scale,
-                                     cfg->norm_min, nullptr, topk_ids, topk_w, counts, s),
-                    "topk");
+    wb = wpk;
   }
-  // fp32 weights: hi/lo split, one GEMM against [2E,H], topk folds the halves.
-  __bf16* wpk = (__bf16*)ws;
-  float* dpk = (float*)((char*)ws + round256((size_t)2 * E * H * 2));
-  rc = launched(moe::launch_wsplit((const float*)w, wpk, E, H, s), "wsplit");
-  if (rc) return rc;
-  rc = launched(moe::launch_router_gemm((const __bf16*)x, wpk, T, H, 2 * E, dpk, s),
+  // parts == 1: the GEMM writes the logits; else it writes [T, parts*E]
+  // partial sums and the scoring kernel adds them and writes the logits.
+  float* gout = parts > 1 ? (float*)wsp : logits;
+  rc = launched(moe::launch_router_gemm((const __bf16*)x, wb, T, H, N, ksplit, gout, s),
                 "router_gemm");
   if (rc) return rc;
-  return launched(moe::launch_topk(dpk, 1, bias, T, E, k, cfg->scoring, cfg->renormalize,
+  return launched(moe::launch_topk(gout, parts, bias, T, E, k, cfg->scoring, cfg->renormalize,
                                    cfg->n_group, cfg->topk_group, cfg->route_scale,
-                                   cfg->norm_min, logits, topk_ids, topk_w, counts, s),
+                                   cfg->norm_min, parts > 1 ? logits : nullptr, topk_ids, topk_w,
+                                   counts, s),
                   "topk");
 }
 

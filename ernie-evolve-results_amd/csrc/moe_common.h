@@ -41,8 +41,9 @@ namespace moe {
 
 hipError_t launch_wsplit(const float* w, __bf16* wpk, int E, int H, hipStream_t s);
 hipError_t launch_router_gemm(const __bf16* x, const __bf16* w, int T, int H, int N,
-                              float* out, hipStream_t s);
-hipError_t launch_topk(const float* logits, int fold, const float* bias, int T, int E, int k,
+                              int ksplit, float* out, hipStream_t s);
+int router_gemm_ksplit(int T, int H, int N);
+hipError_t launch_topk(const float* logits, int nparts, const float* bias, int T, int E, int k,
                        int scoring, int renorm, int n_group, int topk_group, float route_scale,
                        float norm_min, float* logits_out, int32_t* ids, float* w,
                        int32_t* counts, hipStream_t s);
@@ -56,6 +57,9 @@ hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, int T, int 
                              void* xg, float* scales, hipStream_t s);
 hipError_t launch_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* w,
                           const void* shared, int T, int H, int k, void* out, hipStream_t s);
+
+// Experts per lane of the scoring kernel for (E, scoring, n_group).
+int topk_lane_width(int E, int scoring, int n_group);
 
 // Number of pairs one dispatch block ranks (per-block expert bitmasks).
 constexpr int kPairsPerBlock = 256;

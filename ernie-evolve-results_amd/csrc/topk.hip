@@ -2,10 +2,11 @@
 //
 // Replaces the reference's topk_kernel (K:1829-1920).  That kernel gives each
 // token one 32-lane warp with NE=64 experts as two scores per lane.  Here a
-// token gets a group of G = min(64, E) lanes of a 64-lane wavefront, each lane
-// holding V = E / G contiguous experts (one float / float2 / float4 load), so
-// 64/G tokens share a wavefront when E < 64.  Reductions are xor butterflies
-// inside the G-lane group.
+// token gets G = E/V lanes of a 64-lane wavefront, each holding V <= 16
+// contiguous experts (G = 16 at E = 256: four tokens per wavefront), so the
+// cross-lane levels of every reduction are DPP moves within a 16-lane row
+// rather than LDS-routed shuffles, and 16 tokens per 256-thread block give
+// the chip ~8 wavefronts per SIMD at T = 32768.
 //
 // Selection is k rounds of a group argmax with ties to the lower expert index
 // (K:1872-1901), the winner's owner lane masking it out.  Every value feeding
@@ -22,96 +23,89 @@
 namespace moe {
 
 constexpr int kScoreSoftmax = 0, kScoreSigmoidGroup = 1, kScoreSoftmaxBias = 2;
-constexpr int kTopkTokensPerBlock = 64;
 
-template <int E>
-struct TopkShape {
-  static constexpr int V = E <= 64 ? 1 : E / 64;  // experts per lane
-  static constexpr int G = E / V;                 // lanes per token
-  static constexpr int TPW = 64 / G;              // tokens per wavefront pass
-  static constexpr int ITER = kTopkTokensPerBlock / (4 * TPW);
-};
-
-__device__ __forceinline__ float group_max(float v, int G) {
-  for (int o = 1; o < G; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+// Partner value at butterfly level `lvl` inside aligned groups of 2^(lvl+1)
+// lanes.  Levels 0-3 are DPP moves (quad_perm xor1, xor2; row_half_mirror;
+// row_mirror) -- a mirror pairs lane i with the lane holding the other half
+// of its 2^(lvl+1) block, exactly like an xor, so pairwise sums keep the
+// adjacent-pair tree order.  Levels 4-5 cross DPP rows: xor shuffle.
+template <int LVL>
+__device__ __forceinline__ int partner_i(int v) {
+  if constexpr (LVL == 0) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (LVL == 1) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (LVL == 2) return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  else if constexpr (LVL == 3) return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  else return __shfl_xor(v, 1 << LVL, 64);
+}
+template <int LVL>
+__device__ __forceinline__ float partner_f(float v) {
+  return __int_as_float(partner_i<LVL>(__float_as_int(v)));
 }
 
-// Pairwise sum over the G-lane group: lane partials are combined with xor 1,
-// 2, 4, ...; a + b == b + a, so every lane ends with the same bits.
-__device__ __forceinline__ float group_sum(float v, int G) {
-#pragma clang fp contract(off)
-  for (int o = 1; o < G; o <<= 1) v = v + __shfl_xor(v, o, 64);
-  return v;
-}
+// Runtime level -> compile-time partner (levels are uniform across the wave).
+#define MOE_FOR_LEVELS(LO, HI, ...)                                     \
+  {                                                                     \
+    if (0 >= (LO) && 0 < (HI)) { constexpr int L_ = 0; __VA_ARGS__ }   \
+    if (1 >= (LO) && 1 < (HI)) { constexpr int L_ = 1; __VA_ARGS__ }   \
+    if (2 >= (LO) && 2 < (HI)) { constexpr int L_ = 2; __VA_ARGS__ }   \
+    if (3 >= (LO) && 3 < (HI)) { constexpr int L_ = 3; __VA_ARGS__ }   \
+    if (4 >= (LO) && 4 < (HI)) { constexpr int L_ = 4; __VA_ARGS__ }   \
+    if (5 >= (LO) && 5 < (HI)) { constexpr int L_ = 5; __VA_ARGS__ }   \
+  }
 
 template <int V>
 __device__ __forceinline__ float local_pairwise_sum(const float (&e)[V]) {
 #pragma clang fp contract(off)
-  if constexpr (V == 1) return e[0];
-  else if constexpr (V == 2) return e[0] + e[1];
-  else if constexpr (V == 4) return (e[0] + e[1]) + (e[2] + e[3]);
-  else {
-    float s[V];
+  float s[V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) s[j] = e[j];
+  for (int j = 0; j < V; ++j) s[j] = e[j];
 #pragma unroll
-    for (int w = V; w > 1; w >>= 1)
+  for (int w = V; w > 1; w >>= 1)
 #pragma unroll
-      for (int j = 0; j < w / 2; ++j) s[j] = s[2 * j] + s[2 * j + 1];
-    return s[0];
-  }
+    for (int j = 0; j < w / 2; ++j) s[j] = s[2 * j] + s[2 * j + 1];
+  return s[0];
 }
 
-template <int V>
-__device__ __forceinline__ void load_row(const float* __restrict__ p, float (&v)[V]) {
-  if constexpr (V == 4) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
-  } else if constexpr (V == 2) {
-    const float2 a = *reinterpret_cast<const float2*>(p);
-    v[0] = a.x; v[1] = a.y;
-  } else {
-#pragma unroll
-    for (int j = 0; j < V; ++j) v[j] = p[j];
-  }
-}
+constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
 
-template <int E, int SCORING>
+// One token per G = E/V lanes; V contiguous experts per lane; 256 threads,
+// one pass: 4 * 64/G tokens per block.
+template <int E, int V>
 __global__ __launch_bounds__(256) void topk_kernel(
-    const float* __restrict__ logits, int fold, const float* __restrict__ bias, int T, int k,
-    int renorm, int n_group, int topk_group, float route_scale, float norm_min,
+    const float* __restrict__ logits, int nparts, const float* __restrict__ bias, int T, int k,
+    int scoring, int renorm, int n_group, int topk_group, float route_scale, float norm_min,
     float* __restrict__ lout, int* __restrict__ ids, float* __restrict__ wout,
     int* __restrict__ counts) {
 #pragma clang fp contract(off)
-  using S = TopkShape<E>;
-  constexpr int V = S::V, G = S::G, TPW = S::TPW;
+  constexpr int G = E / V;
+  constexpr int LG = ilog2c(G);
+  constexpr int TPB = 4 * (64 / G);
+  static_assert(G >= 8 && G <= 64 && V >= 1 && V <= 16, "lane shape");
   constexpr float NEG_INF = -__builtin_inff();
   __shared__ int hist[E];
   const int tid = threadIdx.x;
-  for (int i = tid; i < E; i += 256) hist[i] = 0;
-  __syncthreads();
+  if (counts) {
+    for (int i = tid; i < E; i += 256) hist[i] = 0;
+    __syncthreads();
+  }
 
-  const int lane = tid & 63, wave = tid >> 6;
-  const int sub = lane / G, gl = lane % G;
-  const int e0 = gl * V;  // first expert of this lane
-  float b[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) b[j] = bias ? bias[e0 + j] : 0.0f;
-  const int in_stride = fold ? 2 * E : E;
-
-  for (int it = 0; it < S::ITER; ++it) {
-    const long long t =
-        (long long)blockIdx.x * kTopkTokensPerBlock + (it * 4 + wave) * TPW + sub;
-    const bool valid = t < T;
-    float l[V];
+  const int gl = tid % G;
+  const long long t = (long long)blockIdx.x * TPB + tid / G;
+  const bool valid = t < T;
+  const int e0 = gl * V;
+  float l[V];
+  {
+    // nparts > 1: the row holds nparts partial sums of the logits side by
+    // side (bf16 hi/lo weight halves, K partitions of the GEMM); they are
+    // added in index order.
+    const int in_stride = nparts * E;
     if (valid) {
-      load_row<V>(logits + t * in_stride + e0, l);
-      if (fold) {
-        float lo[V];
-        load_row<V>(logits + t * in_stride + E + e0, lo);
+      const float* src = logits + t * in_stride + e0;
 #pragma unroll
-        for (int j = 0; j < V; ++j) l[j] = l[j] + lo[j];
+      for (int j = 0; j < V; ++j) l[j] = src[j];
+      for (int p = 1; p < nparts; ++p) {
+#pragma unroll
+        for (int j = 0; j < V; ++j) l[j] = l[j] + src[p * E + j];
       }
       if (lout) {
 #pragma unroll
@@ -121,129 +115,139 @@ __global__ __launch_bounds__(256) void topk_kernel(
 #pragma unroll
       for (int j = 0; j < V; ++j) l[j] = 0.0f;
     }
+  }
+  float b[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) b[j] = bias ? bias[e0 + j] : 0.0f;
 
-    // ---- scores: sel (what is ranked) and aux (what the weight is made of)
-    float sel[V], aux[V];
-    float m0 = 0.0f, fullsum = 1.0f;
-    if constexpr (SCORING == kScoreSoftmax) {
+  // ---- scores: sel (what is ranked) and aux (what the weight is made of)
+  float sel[V], aux[V];
+  float fullsum = 1.0f;
+  if (scoring == kScoreSoftmax) {
 #pragma unroll
-      for (int j = 0; j < V; ++j) { sel[j] = l[j] + b[j]; aux[j] = sel[j]; }
-      if (!renorm) {
-        float m = sel[0];
+    for (int j = 0; j < V; ++j) { sel[j] = l[j] + b[j]; aux[j] = sel[j]; }
+    if (!renorm) {
+      float m = sel[0];
 #pragma unroll
-        for (int j = 1; j < V; ++j) m = fmaxf(m, sel[j]);
-        m = group_max(m, G);
-        float e[V];
-#pragma unroll
-        for (int j = 0; j < V; ++j) e[j] = det_exp(sel[j] - m);
-        fullsum = group_sum(local_pairwise_sum<V>(e), G);
-      }
-    } else if constexpr (SCORING == kScoreSoftmaxBias) {
-      // K:1857-1866: e = exp(l - max), p = e * (1/sum), c = p + bias
-      float m = l[0];
-#pragma unroll
-      for (int j = 1; j < V; ++j) m = fmaxf(m, l[j]);
-      m = group_max(m, G);
+      for (int j = 1; j < V; ++j) m = fmaxf(m, sel[j]);
+      MOE_FOR_LEVELS(0, LG, { m = fmaxf(m, partner_f<L_>(m)); })
       float e[V];
 #pragma unroll
-      for (int j = 0; j < V; ++j) e[j] = det_exp(l[j] - m);
-      const float rs = __fdiv_rn(1.0f, group_sum(local_pairwise_sum<V>(e), G));
+      for (int j = 0; j < V; ++j) e[j] = det_exp(sel[j] - m);
+      float sum = local_pairwise_sum<V>(e);
+      MOE_FOR_LEVELS(0, LG, { sum = sum + partner_f<L_>(sum); })
+      fullsum = sum;
+    }
+  } else if (scoring == kScoreSoftmaxBias) {
+    // K:1857-1866: e = exp(l - max), p = e * (1/sum), c = p + bias
+    float m = l[0];
+#pragma unroll
+    for (int j = 1; j < V; ++j) m = fmaxf(m, l[j]);
+    MOE_FOR_LEVELS(0, LG, { m = fmaxf(m, partner_f<L_>(m)); })
+    float e[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) e[j] = det_exp(l[j] - m);
+    float sum = local_pairwise_sum<V>(e);
+    MOE_FOR_LEVELS(0, LG, { sum = sum + partner_f<L_>(sum); })
+    const float rs = __fdiv_rn(1.0f, sum);
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float p = e[j] * rs;
+      sel[j] = p + b[j];
+      aux[j] = sel[j];
+    }
+  } else {  // sigmoid + selection bias, group-limited
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      aux[j] = det_sigmoid(l[j]);
+      sel[j] = aux[j] + b[j];
+    }
+    if (n_group > 1) {
+      const int lgl = ilog2c((E / n_group) / V);  // log2(lanes per group), V divides the group
+      float t1 = NEG_INF, t2 = NEG_INF;
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        const float p = e[j] * rs;
-        sel[j] = p + b[j];
-        aux[j] = sel[j];
+        const float v = sel[j];
+        if (v > t1) { t2 = t1; t1 = v; }
+        else if (v > t2) t2 = v;
       }
-    } else {  // sigmoid + selection bias, group-limited
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        aux[j] = det_sigmoid(l[j]);
-        sel[j] = aux[j] + b[j];
+      MOE_FOR_LEVELS(0, lgl, {
+        const float o1 = partner_f<L_>(t1), o2 = partner_f<L_>(t2);
+        const float n1 = fmaxf(t1, o1);
+        const float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
+        t1 = n1;
+        t2 = n2;
+      })
+      const float gscore = t1 + t2;
+      const int g = gl >> lgl;
+      bool kept = false;
+      for (int r = 0; r < topk_group; ++r) {
+        float bv = kept ? NEG_INF : gscore;
+        int bg = g;
+        MOE_FOR_LEVELS(lgl, LG, {
+          const float ov = partner_f<L_>(bv);
+          const int og = partner_i<L_>(bg);
+          if (ov > bv || (ov == bv && og < bg)) { bv = ov; bg = og; }
+        })
+        if (bg == g) kept = true;
       }
-      if (n_group > 1) {
-        const int L = (E / n_group) / V;  // lanes per group (>= 1, power of two)
-        float t1 = NEG_INF, t2 = NEG_INF;
+      if (!kept) {
 #pragma unroll
-        for (int j = 0; j < V; ++j) {
-          const float v = sel[j];
-          if (v > t1) { t2 = t1; t1 = v; }
-          else if (v > t2) t2 = v;
-        }
-        for (int o = 1; o < L; o <<= 1) {
-          const float o1 = __shfl_xor(t1, o, 64), o2 = __shfl_xor(t2, o, 64);
-          const float n1 = fmaxf(t1, o1);
-          const float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
-          t1 = n1;
-          t2 = n2;
-        }
-        const float gscore = t1 + t2;
-        const int g = gl / L;
-        bool kept = false;
-        for (int r = 0; r < topk_group; ++r) {
-          float bv = kept ? NEG_INF : gscore;
-          int bg = g;
-          for (int o = L; o < G; o <<= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int og = __shfl_xor(bg, o, 64);
-            if (ov > bv || (ov == bv && og < bg)) { bv = ov; bg = og; }
-          }
-          if (bg == g) kept = true;
-        }
-        if (!kept) {
-#pragma unroll
-          for (int j = 0; j < V; ++j) sel[j] = NEG_INF;
-        }
+        for (int j = 0; j < V; ++j) sel[j] = NEG_INF;
       }
     }
+  }
 
-    // ---- k rounds of group argmax (ties -> lower index, K:1886)
-    int my_id = 0;
-    float my_sel = 0.0f, my_aux = 0.0f;
-    float acc = 0.0f;  // sequential slot-order sum the weights divide by
-    for (int r = 0; r < k; ++r) {
-      float bv = sel[0], ba = aux[0];
-      int bi = e0;
+  // ---- k rounds of group argmax (ties -> lower index, K:1886)
+  int my_id = 0;
+  float my_sel = 0.0f, my_aux = 0.0f, m0 = 0.0f;
+  float acc = 0.0f;  // sequential slot-order sum the weights divide by
+  for (int r = 0; r < k; ++r) {
+    float bv = sel[0], ba = aux[0];
+    int bi = e0;
 #pragma unroll
-      for (int j = 1; j < V; ++j)
-        if (sel[j] > bv) { bv = sel[j]; ba = aux[j]; bi = e0 + j; }
-      for (int o = 1; o < G; o <<= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        const float oa = __shfl_xor(ba, o, 64);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; ba = oa; }
-      }
-      if (gl == r) { my_id = bi; my_sel = bv; my_aux = ba; }
+    for (int j = 1; j < V; ++j)
+      if (sel[j] > bv) { bv = sel[j]; ba = aux[j]; bi = e0 + j; }
+    MOE_FOR_LEVELS(0, LG, {
+      const float ov = partner_f<L_>(bv);
+      const int oi = partner_i<L_>(bi);
+      const float oa = partner_f<L_>(ba);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; ba = oa; }
+    })
+    if (gl == r) { my_id = bi; my_sel = bv; my_aux = ba; }
 #pragma unroll
-      for (int j = 0; j < V; ++j)
-        if (e0 + j == bi) sel[j] = NEG_INF;
-      if constexpr (SCORING == kScoreSoftmax) {
-        if (r == 0) m0 = bv;
-        const float e = det_exp(bv - m0);
-        acc = (r == 0) ? e : acc + e;
-      } else if constexpr (SCORING == kScoreSigmoidGroup) {
-        acc = (r == 0) ? ba : acc + ba;
-      } else {
-        acc = (r == 0) ? bv : acc + bv;
-      }
+    for (int j = 0; j < V; ++j)
+      if (e0 + j == bi) sel[j] = NEG_INF;
+    if (scoring == kScoreSoftmax) {
+      if (r == 0) m0 = bv;
+      const float e = det_exp(bv - m0);
+      acc = (r == 0) ? e : acc + e;
+    } else if (scoring == kScoreSigmoidGroup) {
+      acc = (r == 0) ? ba : acc + ba;
+    } else {
+      acc = (r == 0) ? bv : acc + bv;
     }
+  }
 
+  // lane gl < k holds slot gl (G >= 8 >= k)
+  {
     if (valid && gl < k) {
       float wv;
-      if constexpr (SCORING == kScoreSoftmax) {
+      if (scoring == kScoreSoftmax) {
         const float e = det_exp(my_sel - m0);
         wv = __fdiv_rn(e, renorm ? acc : fullsum) * route_scale;
-      } else if constexpr (SCORING == kScoreSigmoidGroup) {
+      } else if (scoring == kScoreSigmoidGroup) {
         wv = (renorm ? __fdiv_rn(my_aux, acc + 1e-20f) : my_aux) * route_scale;
       } else {
         wv = __fdiv_rn(my_sel, fmaxf(acc, norm_min));  // K:1909
       }
       ids[t * k + gl] = my_id;
       wout[t * k + gl] = wv;
-      atomicAdd(&hist[my_id], 1);
+      if (counts) atomicAdd(&hist[my_id], 1);
     }
   }
-  __syncthreads();
   if (counts) {
+    __syncthreads();
     for (int i = tid; i < E; i += 256) {
       const int c = hist[i];
       if (c) atomicAdd(counts + i, c);
@@ -256,26 +260,33 @@ __global__ void zero_i32_kernel(int* __restrict__ p, int n) {
   if (i < n) p[i] = 0;
 }
 
-template <int E>
-static hipError_t launch_topk_e(const float* logits, int fold, const float* bias, int T, int k,
-                                int scoring, int renorm, int n_group, int topk_group,
-                                float route_scale, float norm_min, float* lout, int32_t* ids,
-                                float* w, int32_t* counts, hipStream_t s) {
-  const dim3 grid((unsigned)((T + kTopkTokensPerBlock - 1) / kTopkTokensPerBlock));
-#define MOE_TOPK_ARGS                                                                      \
-  grid, dim3(256), 0, s, logits, fold, bias, T, k, renorm, n_group, topk_group, route_scale, \
-      norm_min, lout, ids, w, counts
-  if (scoring == kScoreSoftmax)
-    hipLaunchKernelGGL((topk_kernel<E, kScoreSoftmax>), MOE_TOPK_ARGS);
-  else if (scoring == kScoreSigmoidGroup)
-    hipLaunchKernelGGL((topk_kernel<E, kScoreSigmoidGroup>), MOE_TOPK_ARGS);
-  else
-    hipLaunchKernelGGL((topk_kernel<E, kScoreSoftmaxBias>), MOE_TOPK_ARGS);
-#undef MOE_TOPK_ARGS
+template <int E, int V>
+static hipError_t launch_topk_ev(const float* logits, int nparts, const float* bias, int T, int k,
+                                 int scoring, int renorm, int n_group, int topk_group,
+                                 float route_scale, float norm_min, float* lout, int32_t* ids,
+                                 float* w, int32_t* counts, hipStream_t s) {
+  constexpr int TPB = 4 * (64 / (E / V));
+  const dim3 grid((unsigned)((T + TPB - 1) / TPB));
+  hipLaunchKernelGGL((topk_kernel<E, V>), grid, dim3(256), 0, s, logits, nparts, bias, T, k,
+                     scoring, renorm, n_group, topk_group, route_scale, norm_min, lout, ids, w,
+                     counts);
   return hipGetLastError();
 }
 
-hipError_t launch_topk(const float* logits, int fold, const float* bias, int T, int E, int k,
+// Experts per lane V = min(16, E/8, expert-group size): a token spans
+// G = E/V lanes, at least 8 so every slot (k <= 8) has its own lane, at most
+// 16 for E <= 256 so every reduction level is a DPP move; an expert group
+// never splits a lane.
+int topk_lane_width(int E, int scoring, int n_group) {
+  int V = E / 8 < 16 ? E / 8 : 16;
+  if (scoring == kScoreSigmoidGroup && n_group > 1) {
+    const int gs = E / n_group;
+    if (gs < V) V = gs;
+  }
+  return V < 1 ? 1 : V;
+}
+
+hipError_t launch_topk(const float* logits, int nparts, const float* bias, int T, int E, int k,
                        int scoring, int renorm, int n_group, int topk_group, float route_scale,
                        float norm_min, float* lout, int32_t* ids, float* w, int32_t* counts,
                        hipStream_t s) {
@@ -285,21 +296,27 @@ hipError_t launch_topk(const float* logits, int fold, const float* bias, int T, 
     if (err != hipSuccess) return err;
   }
   if (T == 0) return hipSuccess;
-#define MOE_TOPK_CASE(EE)                                                                   \
-  case EE:                                                                                  \
-    return launch_topk_e<EE>(logits, fold, bias, T, k, scoring, renorm, n_group, topk_group, \
-                             route_scale, norm_min, lout, ids, w, counts, s);
-  switch (E) {
-    MOE_TOPK_CASE(8)
-    MOE_TOPK_CASE(16)
-    MOE_TOPK_CASE(32)
-    MOE_TOPK_CASE(64)
-    MOE_TOPK_CASE(128)
-    MOE_TOPK_CASE(256)
-    default:
-      return hipErrorInvalidValue;
-  }
+  const int V = topk_lane_width(E, scoring, n_group);
+#define MOE_TOPK_CASE(EE, VV)                                                               \
+  if (E == EE && V == VV)                                                                   \
+    return launch_topk_ev<EE, VV>(logits, nparts, bias, T, k, scoring, renorm, n_group,       \
+                                  topk_group, route_scale, norm_min, lout, ids, w, counts, s);
+  MOE_TOPK_CASE(8, 1)
+  MOE_TOPK_CASE(16, 2)
+  MOE_TOPK_CASE(32, 2)
+  MOE_TOPK_CASE(32, 4)
+  MOE_TOPK_CASE(64, 2)
+  MOE_TOPK_CASE(64, 4)
+  MOE_TOPK_CASE(64, 8)
+  MOE_TOPK_CASE(128, 2)
+  MOE_TOPK_CASE(128, 4)
+  MOE_TOPK_CASE(128, 8)
+  MOE_TOPK_CASE(128, 16)
+  MOE_TOPK_CASE(256, 4)
+  MOE_TOPK_CASE(256, 8)
+  MOE_TOPK_CASE(256, 16)
 #undef MOE_TOPK_CASE
+  return hipErrorInvalidValue;
 }
 
 }  // namespace moe

@@ -320,10 +320,14 @@ class MoePlan:
         self.nws_perm = L.moe_permute_workspace_bytes(T, E, k)
         self.ws_perm = torch.empty(max(self.nws_perm, 256), dtype=torch.uint8, device=dev)
 
-    def route(self, x, w, bias):
+    def route(self, x, w, bias, counts=False):
+        """Router GEMM + scoring + top-k.  The per-expert counts are also
+        produced by ``permute``; ``counts=True`` additionally fills
+        ``route_counts`` from the scoring kernel's histogram."""
         _check(lib().moe_route(_ptr(x), _ptr(w), self.wd, _ptr(bias), self.T, self.H, self.E,
                                self.k, ctypes.byref(self.cfg), _ptr(self.logits),
-                               _ptr(self.topk_ids), _ptr(self.topk_w), _ptr(self.route_counts),
+                               _ptr(self.topk_ids), _ptr(self.topk_w),
+                               _ptr(self.route_counts) if counts else None,
                                _ptr(self.ws_route), self.nws_route, _stream(x)))
 
     def router_gemm(self, x, w):

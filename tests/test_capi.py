@@ -109,6 +109,9 @@ def test_workspace_sizes():
     assert L.moe_route_workspace_bytes(100, 128, 8, 0) == 0
     # fp32 weights: [2E,H] bf16 split + [T,2E] fp32 logits, each 256-aligned
     assert L.moe_route_workspace_bytes(100, 128, 8, 1) == 4096 + 6400
+    # DeepSeek-V3 shape: the GEMM splits K in two -> [T, 2E] fp32 partial sums
+    assert L.moe_route_workspace_bytes(32768, 7168, 256, 0) == 32768 * 2 * 256 * 4
+    assert L.moe_route_workspace_bytes(65536, 7168, 256, 0) == 0
     # T*k = 32768*8 pairs -> 1024 blocks of 256; [E, nblk] + [E] int32
     assert L.moe_permute_workspace_bytes(32768, 256, 8) == 256 * 1024 * 4 + 1024
 
