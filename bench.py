@@ -46,6 +46,22 @@ def algorithmic_bytes(c):
                 + T * E * 4)
 
 
+def measured_traffic():
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (copy-calibrated), read from the committed summary: lines
+    `traffic <kernel> <bytes>` of profiles/c4_hbm_traffic.md."""
+    out = {}
+    try:
+        with open(os.path.join(REPO, "profiles", "c4_hbm_traffic.md")) as f:
+            for line in f:
+                p = line.split()
+                if len(p) == 3 and p[0] == "traffic":
+                    out[p[1]] = float(p[2])
+    except OSError:
+        pass
+    return out
+
+
 def cpu_baseline(c, sample_T):
     """The CPU oracle (oracle/moe_oracle.py) on `sample_T` tokens of the same
     workload: router GEMM (torch fp32), scoring/top-k, permutation, gather /
@@ -115,35 +131,47 @@ def main():
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
 
-    # ---- per-stage HIP-event timing (same stream the kernels run on)
+    # ---- per-stage HIP-event timing (on the stream the kernels run on).
+    # permute = 3 index kernels + the gather launch; an index-only permute
+    # (no rows) isolates the gather.  route = GEMM + scoring; a standalone
+    # scoring launch on the finished logits isolates the GEMM.
     ev = lambda: torch.cuda.Event(enable_timing=True)
-    st = {"router_gemm": [], "route": [], "permute": [], "combine": []}
+    st = {"route": [], "permute": [], "permute_index": [], "combine": [], "topk": []}
     for _ in range(args.steps):
-        e = [ev() for _ in range(5)]
+        e = [ev() for _ in range(6)]
         e[0].record()
-        plan.router_gemm(x, w)
-        e[1].record()
         plan.route(x, w, bias)
-        e[2].record()
+        e[1].record()
         plan.permute(x)
-        e[3].record()
+        e[2].record()
         plan.combine(y)
+        e[3].record()
+        plan.permute(x, index_only=True)
         e[4].record()
+        plan.topk_only(bias)
+        e[5].record()
         torch.cuda.synchronize()
-        st["router_gemm"].append(e[0].elapsed_time(e[1]) * 1e3)
-        st["route"].append(e[1].elapsed_time(e[2]) * 1e3)
-        st["permute"].append(e[2].elapsed_time(e[3]) * 1e3)
-        st["combine"].append(e[3].elapsed_time(e[4]) * 1e3)
+        st["route"].append(e[0].elapsed_time(e[1]) * 1e3)
+        st["permute"].append(e[1].elapsed_time(e[2]) * 1e3)
+        st["combine"].append(e[2].elapsed_time(e[3]) * 1e3)
+        st["permute_index"].append(e[3].elapsed_time(e[4]) * 1e3)
+        st["topk"].append(e[4].elapsed_time(e[5]) * 1e3)
     us = {k2: statistics.mean(v) for k2, v in st.items()}
+    us["gather"] = us["permute"] - us["permute_index"]
+    us["router_gemm"] = max(us["route"] - us["topk"], 1e-3)
 
     ab = algorithmic_bytes(c)
-    # dominant kernel: the single-launch combine or the permute's gather
-    # (permute = 3 small index kernels + the gather launch)
-    comb_gbs = ab["combine"] / (us["combine"] * 1e-6) / 1e9
-    roofline = {"kernel": "combine_kernel", "bound": "hbm", "achieved": round(comb_gbs, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(comb_gbs / HBM_PEAK_GBS, 4),
-                "traffic": None, "algorithmic_bytes": ab["combine"],
-                "avg_launch_us": round(us["combine"], 2)}
+    traffic = measured_traffic()
+    kern = {"combine": ("combine_wave_kernel", ab["combine"], us["combine"]),
+            "gather": ("gather_fp8_kernel" if c.fp8 else "gather_kernel", ab["gather"],
+                       us["gather"])}
+    dom = max(kern, key=lambda n: kern[n][2])
+    kname, kbytes, kus = kern[dom]
+    gbs = kbytes / (kus * 1e-6) / 1e9
+    tr = traffic.get(kname) if c.name in ("C4",) else None
+    roofline = {"kernel": kname, "bound": "hbm", "achieved": round(gbs, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                "traffic": tr, "algorithmic_bytes": kbytes, "avg_launch_us": round(kus, 2)}
     total_bytes = ab["route"] + ab["gather"] + ab["combine"]
     e2e_gbs = total_bytes / (ms_per_step * 1e-3) / 1e9
     flops = 2.0 * c.T * c.H * c.E
@@ -172,7 +200,8 @@ def main():
         "stage_hbm_frac": {
             "route": round(ab["route"] / (us["route"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "permute": round(ab["gather"] / (us["permute"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "combine": round(comb_gbs / HBM_PEAK_GBS, 4)},
+            "gather": round(ab["gather"] / (us["gather"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "combine": round(ab["combine"] / (us["combine"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
         "router_gemm": gemm,
         "cpu_baseline": cpu,
     }

@@ -334,10 +334,17 @@ class MoePlan:
         _check(lib().moe_router_gemm(_ptr(x), _ptr(w), self.T, self.H, self.E, _ptr(self.logits),
                                      _stream(x)))
 
-    def permute(self, x):
+    def topk_only(self, bias):
+        """Scoring + top-k on the current ``logits`` (used to time the stage)."""
+        _check(lib().moe_topk(_ptr(self.logits), _ptr(bias), self.T, self.E, self.k,
+                              ctypes.byref(self.cfg), _ptr(self.topk_ids), _ptr(self.topk_w), None,
+                              _stream(self.logits)))
+
+    def permute(self, x, index_only=False):
         od = DTYPE_FP8E4M3FN if self.fp8 else self.xd
         _check(lib().moe_permute(_ptr(x), self.xd, _ptr(self.topk_ids), self.T, self.H, self.E,
-                                 self.k, od, _ptr(self.xg), _ptr(self.scales),
+                                 self.k, od, None if index_only else _ptr(self.xg),
+                                 _ptr(self.scales),
                                  _ptr(self.row_token), _ptr(self.pair_row), _ptr(self.offsets),
                                  _ptr(self.counts), _ptr(self.ws_perm), self.nws_perm,
                                  _stream(x)))
