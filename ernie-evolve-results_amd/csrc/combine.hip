@@ -87,11 +87,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const u32x4* __restrict__ 
 }
 
 // Wave-chunk variant: a wavefront owns VPW * 64 consecutive vectors of ONE
-// output row (needs nvec % (VPW*64) == 0, e.g. H % 1024 == 0 for bf16), so the
-// row's k indices and weights are wave-uniform (scalar registers) and each
-// lane keeps VPW * k independent 16-byte loads in flight, every one part of
-// a 1 KB contiguous wave access.  Measured on MI355X at the DeepSeek-V3 shape:
-// ~4% faster than the flat mapping.
+// output row (needs nvec % (VPW*64) == 0, e.g. H % 512 == 0 for bf16 at
+// VPW = 1), so the row's k indices and weights are wave-uniform (scalar
+// registers) and each lane keeps VPW * k independent 16-byte loads in flight,
+// every one part of a 1 KB contiguous wave access.  Measured on MI355X at the
+// DeepSeek-V3 shape: within ~3% of a synthetic kernel with the same byte mix
+// (8 sequential read streams + 1 write stream, 731 us).
 template <int K, bool BF16, int VPW>
 __global__ __launch_bounds__(256) void combine_wave_kernel(const u32x4* __restrict__ y,
                                                            const int* __restrict__ pair_row,
@@ -153,12 +154,16 @@ static hipError_t launch_combine_t(const void* y, const int32_t* pair_row, const
   const u32x4* ys = (const u32x4*)y;
   const u32x4* sh = (const u32x4*)shared;
   u32x4* o = (u32x4*)out;
-  const bool wave = nvec % 128 == 0;
-  const dim3 wgrid(4096);
+  // one 64-vector chunk per wave, about one pass of blocks over the rows
+  // (measured faster than a small grid looping over many chunks)
+  const bool wave = nvec % 64 == 0;
+  long long wg = ((long long)total / 64 + 3) / 4;
+  if (wg > 65536) wg = 65536;
+  const dim3 wgrid((unsigned)(wg < 1 ? 1 : wg));
 #define MOE_COMBINE_CASE(KK)                                                                   \
   case KK:                                                                                     \
     if (wave)                                                                                  \
-      hipLaunchKernelGGL((combine_wave_kernel<KK, BF16, 2>), wgrid, blk, 0, s, ys, pair_row, w,  \
+      hipLaunchKernelGGL((combine_wave_kernel<KK, BF16, 1>), wgrid, blk, 0, s, ys, pair_row, w,  \
                          sh, total, nvec, o);                                                  \
     else                                                                                       \
       hipLaunchKernelGGL((combine_kernel<KK, BF16>), grid, blk, 0, s, ys, pair_row, w, sh,       \
