@@ -6,7 +6,7 @@
 // a lane feeds 8 consecutive k of one row of A and the same 8 k of one
 // column of B, so a fragment is a single 16-byte LDS read.
 //
-// Main kernel (N >= 64): tiles are brought into LDS by the gfx950
+// Tiles are brought into LDS by the gfx950
 // global_load_lds_dwordx4 DMA (no register staging), into an NS-stage ring
 // with an XOR-swizzled 16-byte-chunk layout (conflict-free fragment reads),
 // one s_barrier per K step.  At N = 256 a 512-thread block owns 256 rows x
@@ -19,8 +19,8 @@
 // than 8 waves with 128x64 tiles (measured 122 vs 141 us at T = 32768).
 // x is loaded with the non-temporal bit: it streams through once.
 //
-// Small N (8..32) keeps a plain register-staged kernel: there the GEMM is a
-// pure x stream.
+// Smaller N use smaller row tiles (and split-K when even those leave the
+// chip idle): there the router weight is small and the GEMM is an x stream.
 #include "moe_common.h"
 
 namespace moe {
@@ -47,113 +47,6 @@ hipError_t launch_wsplit(const float* w, __bf16* wpk, int E, int H, hipStream_t 
   const int grid = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
   hipLaunchKernelGGL(wsplit_kernel, dim3(grid), dim3(256), 0, s, w, (unsigned short*)wpk, n);
   return hipGetLastError();
-}
-
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__(256) void router_gemm_kernel(const __bf16* __restrict__ x,
-                                                          const __bf16* __restrict__ w,
-                                                          int T, int H, int N,
-                                                          float* __restrict__ out) {
-  constexpr int BK = 64;
-  constexpr int LDK = BK + 8;  // padded LDS row, elements
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 16, FN = WTN / 16;
-  constexpr int A_VEC = BM * (BK / 8), B_VEC = BN * (BK / 8);  // 16-byte vectors per tile
-  constexpr int A_PER = (A_VEC + 255) / 256, B_PER = (B_VEC + 255) / 256;
-  static_assert(WM * WN == 4, "4 waves");
-  static_assert(FM >= 1 && FN >= 1, "wave tile below one MFMA tile");
-
-  __shared__ __attribute__((aligned(16))) __bf16 sA[BM * LDK];
-  __shared__ __attribute__((aligned(16))) __bf16 sB[BN * LDK];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  const long long m0 = (long long)blockIdx.x * BM;
-  const int n0 = blockIdx.y * BN;
-
-  u32x4 ra[A_PER], rb[B_PER];
-  auto gload = [&](int kt) {
-    const long long kofs = (long long)kt * BK;
-#pragma unroll
-    for (int i = 0; i < A_PER; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx >> 3, c = idx & 7;
-      const long long row = m0 + r;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (idx < A_VEC && row < T)
-        v = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(x + row * H + kofs + c * 8));
-      ra[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < B_PER; ++i) {
-      const int idx = tid + i * 256;
-      const int r = idx >> 3, c = idx & 7;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (idx < B_VEC && n0 + r < N)
-        v = *reinterpret_cast<const u32x4*>(w + (long long)(n0 + r) * H + kofs + c * 8);
-      rb[i] = v;
-    }
-  };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < A_PER; ++i) {
-      const int idx = tid + i * 256;
-      if (idx < A_VEC)
-        *reinterpret_cast<u32x4*>(sA + (idx >> 3) * LDK + (idx & 7) * 8) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < B_PER; ++i) {
-      const int idx = tid + i * 256;
-      if (idx < B_VEC)
-        *reinterpret_cast<u32x4*>(sB + (idx >> 3) * LDK + (idx & 7) * 8) = rb[i];
-    }
-  };
-
-  f32x4 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  const int KT = H / BK;
-  const int frow = lane & 15, fk = (lane >> 4) * 8;
-  gload(0);
-  for (int kt = 0; kt < KT; ++kt) {
-    sstore();
-    __syncthreads();
-    if (kt + 1 < KT) gload(kt + 1);
-#pragma unroll
-    for (int kk = 0; kk < BK; kk += 32) {
-      bf16x8 a[FM], b[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        a[i] = *reinterpret_cast<const bf16x8*>(sA + (wm * WTM + i * 16 + frow) * LDK + kk + fk);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        b[j] = *reinterpret_cast<const bf16x8*>(sB + (wn * WTN + j * 16 + frow) * LDK + kk + fk);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-
-  // 16x16 accumulator layout: lane holds column (lane & 15), rows 4*(lane >> 4) + r.
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int col = n0 + wn * WTN + j * 16 + (lane & 15);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const long long row = m0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
-        if (row < T && col < N) out[row * N + col] = acc[i][j][r];
-      }
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -271,41 +164,45 @@ __global__ __launch_bounds__(64 * WM * WN) void router_gemm_dma_kernel(
     }
 }
 
-template <int BM, int BN, int WM, int WN>
-static hipError_t launch_cfg(const __bf16* x, const __bf16* w, int T, int H, int N, float* out,
-                             hipStream_t s) {
-  const dim3 grid((unsigned)((T + BM - 1) / BM), (unsigned)((N + BN - 1) / BN));
-  hipLaunchKernelGGL((router_gemm_kernel<BM, BN, WM, WN>), grid, dim3(256), 0, s, x, w, T, H, N,
-                     out);
-  return hipGetLastError();
-}
-
 template <int BM, int BN, int NS, int WM, int WN>
 static hipError_t launch_dma(const __bf16* x, const __bf16* w, int T, int H, int N, int ksplit,
                              float* out, hipStream_t s) {
-  const dim3 grid((unsigned)((T + BM - 1) / BM), (unsigned)(N / BN), (unsigned)ksplit);
+  const dim3 grid((unsigned)((T + BM - 1) / BM), (unsigned)((N + BN - 1) / BN), (unsigned)ksplit);
   hipLaunchKernelGGL((router_gemm_dma_kernel<BM, BN, NS, WM, WN>), grid, dim3(64 * WM * WN), 0,
                      s, x, w, T, H, N, H / ksplit, out, N * ksplit);
   return hipGetLastError();
 }
 
-// Number of K partitions the GEMM uses for (T, H, N): 2 when the 256-row
-// blocks alone would leave CUs idle, else 1.  The partial sums are [T, ksplit*N].
+// Tile configuration per N, and the K partition count that fills the chip.
+//   N >= 256: 256 x 256 tile, 16 waves (W re-read once per 256 rows)
+//   N = 128, 64, 32: 64-row tiles, 4 waves (W is small and stays in L2)
+//   N = 16 / 8: 32 x 16 tile, 2 waves (a pure x stream)
+// ksplit doubles while blocks * ksplit is below the target and H still
+// splits into whole 64-wide K steps; the partial sums are [T, ksplit*N].
+struct GemmTile { int bm, bn, target; };
+static GemmTile gemm_tile(int N) {
+  if (N >= 256) return {256, 256, 256};
+  if (N >= 32) return {64, N, 256};
+  return {32, 16, 1024};
+}
+
 int router_gemm_ksplit(int T, int H, int N) {
-  if (N < 256 || N % 256 != 0) return 1;
-  const long long blocks = (long long)((T + 255) / 256) * (N / 256);
-  return (blocks < 256 && H % 128 == 0) ? 2 : 1;
+  const GemmTile g = gemm_tile(N);
+  const long long blocks = (long long)((T + g.bm - 1) / g.bm) * ((N + g.bn - 1) / g.bn);
+  int ks = 1;
+  while (blocks * ks < g.target && ks < 8 && H % (64 * ks * 2) == 0) ks *= 2;
+  return ks;
 }
 
 // N in {8, 16, 32, 64, 128} or a multiple of 256; H % 64 == 0 (checked by
-// the caller).  ksplit > 1 only for N % 256 == 0 and H % (64 * ksplit) == 0.
+// the caller); H % (64 * ksplit) == 0.
 hipError_t launch_router_gemm(const __bf16* x, const __bf16* w, int T, int H, int N, int ksplit,
                               float* out, hipStream_t s) {
   if (N >= 256) return launch_dma<256, 256, 2, 4, 4>(x, w, T, H, N, ksplit, out, s);
-  if (N == 128) return launch_dma<256, 128, 2, 4, 2>(x, w, T, H, N, 1, out, s);
-  if (N == 64) return launch_dma<128, 64, 3, 2, 2>(x, w, T, H, N, 1, out, s);
-  if (N == 32) return launch_cfg<64, 32, 4, 1>(x, w, T, H, N, out, s);
-  return launch_cfg<64, 16, 4, 1>(x, w, T, H, N, out, s);
+  if (N == 128) return launch_dma<64, 128, 3, 1, 4>(x, w, T, H, N, ksplit, out, s);
+  if (N == 64) return launch_dma<64, 64, 3, 2, 2>(x, w, T, H, N, ksplit, out, s);
+  if (N == 32) return launch_dma<64, 32, 3, 4, 1>(x, w, T, H, N, ksplit, out, s);
+  return launch_dma<32, 16, 4, 2, 1>(x, w, T, H, N, ksplit, out, s);
 }
 
 }  // namespace moe

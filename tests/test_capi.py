@@ -106,9 +106,12 @@ def test_permute_and_combine_validation():
 
 def test_workspace_sizes():
     L = M.lib()
-    assert L.moe_route_workspace_bytes(100, 128, 8, 0) == 0
-    # fp32 weights: [2E,H] bf16 split + [T,2E] fp32 logits, each 256-aligned
-    assert L.moe_route_workspace_bytes(100, 128, 8, 1) == 4096 + 6400
+    # small N: 32-row tiles, 4 blocks at T=100 -> K split in 2 (H=128 allows no more)
+    # -> [T, 2E] fp32 partial sums
+    assert L.moe_route_workspace_bytes(100, 128, 8, 0) == 6400
+    # fp32 weights: [2E,H] bf16 split (4096 B) + [T, 2 halves * 2 K parts * E] fp32
+    assert L.moe_route_workspace_bytes(100, 128, 8, 1) == 4096 + 12800
+    assert L.moe_route_workspace_bytes(100, 64, 8, 0) == 0        # H=64: one K step, no split
     # DeepSeek-V3 shape: the GEMM splits K in two -> [T, 2E] fp32 partial sums
     assert L.moe_route_workspace_bytes(32768, 7168, 256, 0) == 32768 * 2 * 256 * 4
     assert L.moe_route_workspace_bytes(65536, 7168, 256, 0) == 0

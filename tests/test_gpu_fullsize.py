@@ -1,0 +1,113 @@
+"""Full-size (BASELINE.json shapes) GPU checks through size-independent
+properties: selection exactness on the GPU's own logits, histogram/offset
+consistency, permutation bijection + stability, bit-equal gathered rows,
+fp8 rows against the oracle on a sample, combine against a torch fp32
+reference, determinism.  Needs an MI355X."""
+import numpy as np
+import pytest
+import torch
+
+import moe_route as M
+from moe_route.configs import CONFIGS
+from oracle import moe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def ocfg(c):
+    return O.RouteCfg(c.scoring, c.renormalize, c.n_group, c.topk_group, c.route_scale,
+                      c.norm_min)
+
+
+def check_permutation_props(ids, p, E, T, k):
+    """counts = bincount, offsets = exclusive cumsum, pair_row a bijection with
+    row_token[pair_row[t*k+j]] == t, and rows of each expert in ascending token
+    order (the stable order)."""
+    flat = ids.reshape(-1).long()
+    counts = torch.bincount(flat, minlength=E)
+    assert torch.equal(p["counts"].long(), counts)
+    offs = torch.zeros(E + 1, dtype=torch.long, device=ids.device)
+    offs[1:] = torch.cumsum(counts, 0)
+    assert torch.equal(p["offsets"].long(), offs)
+    pr = p["pair_row"].long()
+    assert torch.equal(torch.sort(pr).values, torch.arange(T * k, device=ids.device))
+    rt = p["row_token"].long()
+    assert torch.equal(rt[pr], torch.arange(T * k, device=ids.device) // k)
+    # expert of each row, then (expert, token) must be non-decreasing / increasing
+    exp_of_row = torch.empty_like(flat)
+    exp_of_row[pr] = flat
+    key = exp_of_row * T + rt
+    assert bool((key[1:] > key[:-1]).all())
+
+
+def combine_ref(y, pair_row, w, T, k, chunk=2048):
+    out = torch.empty(T, y.shape[1], dtype=torch.float32, device=y.device)
+    pr = pair_row.long().view(T, k)
+    for a in range(0, T, chunk):
+        b = min(T, a + chunk)
+        acc = torch.zeros(b - a, y.shape[1], dtype=torch.float32, device=y.device)
+        for j in range(k):
+            acc += w[a:b, j:j + 1] * y[pr[a:b, j]].float()
+        out[a:b] = acc
+    return out
+
+
+@pytest.mark.parametrize("name", ["C2", "C3", "C4"])
+def test_full_size_route_dispatch_combine(cuda, name):
+    c = CONFIGS[name]
+    x, w, bias, y = M.make_inputs(c, seed=0, device=cuda)
+    r = M.route_dispatch_combine(x, w, bias, y, c.k, c.cfg)
+    torch.cuda.synchronize()
+    T, E, k = c.T, c.E, c.k
+    # logits: float64 reference on a row sample, fp32 summation bound
+    rows = torch.arange(0, T, max(1, T // 256), device=cuda)
+    xd, wd = x[rows].double().cpu(), w.double().cpu()
+    err = (r["logits"][rows].double().cpu() - xd @ wd.t()).abs()
+    bound = c.H * 2.0 ** -24 * (xd.abs() @ wd.abs().t())
+    assert bool((err <= bound).all())
+    # selection on the GPU's own logits: bit-exact ids, weights within 1e-5
+    oi, ow = O.score_topk(r["logits"].cpu().numpy(), None if bias is None else bias.cpu().numpy(),
+                          k, ocfg(c.cfg))
+    assert np.array_equal(r["topk_ids"].cpu().numpy(), oi)
+    got_w = r["topk_w"].cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(got_w - ow) <= 1e-5 * np.abs(ow))
+    assert torch.equal(r["route_counts"], r["counts"])
+    check_permutation_props(r["topk_ids"], r, E, T, k)
+    assert torch.equal(r["xg"], x[r["row_token"].long()])
+    ref = combine_ref(y, r["pair_row"], r["topk_w"], T, k)
+    mag = combine_ref(y.abs(), r["pair_row"], r["topk_w"].abs(), T, k)
+    tol = ref.abs() * 2.0 ** -7 + mag * 2.0 ** -19 + 1e-30
+    assert bool(((r["out"].float() - ref).abs() <= tol).all())
+
+
+def test_full_size_fp8_dispatch_c5(cuda):
+    c = CONFIGS["C5"]
+    x, w, bias, _ = M.make_inputs(c, seed=0, device=cuda, with_y=False)
+    logits, ids, wts, _ = M.route(x, w, bias, c.k, c.cfg)
+    p = M.permute(x, ids, c.E, fp8=True)
+    torch.cuda.synchronize()
+    check_permutation_props(ids, p, c.E, c.T, c.k)
+    # oracle on a sample of routed rows (CPU)
+    rows = torch.arange(0, c.T * c.k, 97, device=cuda)
+    toks = p["row_token"][rows].long()
+    q, s = O.fp8_quant_rows(x[toks].cpu())
+    assert torch.equal(p["xg"][rows].cpu(), q)
+    assert torch.equal(p["scales"][rows].cpu(), s)
+    # dequantised rows reproduce x within e4m3 rounding: half a spacing, i.e.
+    # 2^-4 relative for normals, 2^-10 * scale for e4m3 subnormals
+    sc = p["scales"][rows][..., None]
+    deq = p["xg"][rows].view(torch.float8_e4m3fn).float().view(len(rows), -1, 128) * sc
+    ref = x[toks].float().view(len(rows), -1, 128)
+    assert bool(((deq - ref).abs() <= ref.abs() * 2.0 ** -4 * 1.0001 + sc * 2.0 ** -10).all())
+
+
+def test_full_size_deterministic(cuda):
+    c = CONFIGS["C4"]
+    x, w, bias, y = M.make_inputs(c, seed=1, device=cuda)
+    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, cuda)
+    plan.step(x, w, bias, y)
+    a = {n: getattr(plan, n).clone() for n in ("logits", "topk_ids", "topk_w", "pair_row", "out")}
+    plan.step(x, w, bias, y)
+    torch.cuda.synchronize()
+    for n, v in a.items():
+        assert torch.equal(getattr(plan, n), v), n
