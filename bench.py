@@ -46,13 +46,18 @@ def algorithmic_bytes(c):
                 + T * E * 4)
 
 
-def measured_traffic():
+TRAFFIC_FILES = {"C4": "c4_hbm_traffic.md", "C5": "c5_fp8_dispatch_hbm_traffic.md"}
+
+
+def measured_traffic(config):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    (copy-calibrated), read from the committed summary: lines
-    `traffic <kernel> <bytes>` of profiles/c4_hbm_traffic.md."""
+    (copy-calibrated), read from the committed summary of this workload:
+    lines `traffic <kernel> <bytes>` of profiles/<file>."""
     out = {}
+    if config not in TRAFFIC_FILES:
+        return out
     try:
-        with open(os.path.join(REPO, "profiles", "c4_hbm_traffic.md")) as f:
+        with open(os.path.join(REPO, "profiles", TRAFFIC_FILES[config])) as f:
             for line in f:
                 p = line.split()
                 if len(p) == 3 and p[0] == "traffic":
@@ -161,14 +166,14 @@ def main():
     us["router_gemm"] = max(us["route"] - us["topk"], 1e-3)
 
     ab = algorithmic_bytes(c)
-    traffic = measured_traffic()
+    traffic = measured_traffic(c.name)
     kern = {"combine": ("combine_wave_kernel", ab["combine"], us["combine"]),
             "gather": ("gather_fp8_kernel" if c.fp8 else "gather_kernel", ab["gather"],
                        us["gather"])}
     dom = max(kern, key=lambda n: kern[n][2])
     kname, kbytes, kus = kern[dom]
     gbs = kbytes / (kus * 1e-6) / 1e9
-    tr = traffic.get(kname) if c.name in ("C4",) else None
+    tr = traffic.get(kname)
     roofline = {"kernel": kname, "bound": "hbm", "achieved": round(gbs, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                 "traffic": tr, "algorithmic_bytes": kbytes, "avg_launch_us": round(kus, 2)}

@@ -69,7 +69,8 @@ __global__ __launch_bounds__(64 * WM * WN) void router_gemm_dma_kernel(
   static_assert(FM >= 1 && FN >= 1, "wave tile below one MFMA tile");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave index as a scalar: the A/B choice of each DMA below is a uniform branch
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const long long m0 = (long long)blockIdx.x * BM;
   const int n0 = blockIdx.y * BN;

@@ -68,11 +68,38 @@ __device__ __forceinline__ float local_pairwise_sum(const float (&e)[V]) {
 
 constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
 
+// V contiguous floats; 16-byte accesses when V is a multiple of 4 (a lane's
+// first expert is V-aligned and rows are E floats, so they are aligned).
+template <int V>
+__device__ __forceinline__ void load_vec(const float* __restrict__ p, float (&v)[V]) {
+  if constexpr (V % 4 == 0) {
+#pragma unroll
+    for (int j = 0; j < V; j += 4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(p + j);
+      v[j] = a[0]; v[j + 1] = a[1]; v[j + 2] = a[2]; v[j + 3] = a[3];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = p[j];
+  }
+}
+template <int V>
+__device__ __forceinline__ void store_vec(float* __restrict__ p, const float (&v)[V]) {
+  if constexpr (V % 4 == 0) {
+#pragma unroll
+    for (int j = 0; j < V; j += 4)
+      *reinterpret_cast<f32x4*>(p + j) = (f32x4){v[j], v[j + 1], v[j + 2], v[j + 3]};
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) p[j] = v[j];
+  }
+}
+
 // One token per G = E/V lanes; V contiguous experts per lane; 256 threads,
 // one pass: 4 * 64/G tokens per block.
-template <int E, int V>
+template <int E, int V, int KK>
 __global__ __launch_bounds__(256) void topk_kernel(
-    const float* __restrict__ logits, int nparts, const float* __restrict__ bias, int T, int k,
+    const float* __restrict__ logits, int nparts, const float* __restrict__ bias, int T, int k_rt,
     int scoring, int renorm, int n_group, int topk_group, float route_scale, float norm_min,
     float* __restrict__ lout, int* __restrict__ ids, float* __restrict__ wout,
     int* __restrict__ counts) {
@@ -82,6 +109,7 @@ __global__ __launch_bounds__(256) void topk_kernel(
   constexpr int TPB = 4 * (64 / G);
   static_assert(G >= 8 && G <= 64 && V >= 1 && V <= 16, "lane shape");
   constexpr float NEG_INF = -__builtin_inff();
+  const int k = KK > 0 ? KK : k_rt;  // compile-time for the common k: the rounds unroll
   __shared__ int hist[E];
   const int tid = threadIdx.x;
   if (counts) {
@@ -101,16 +129,14 @@ __global__ __launch_bounds__(256) void topk_kernel(
     const int in_stride = nparts * E;
     if (valid) {
       const float* src = logits + t * in_stride + e0;
-#pragma unroll
-      for (int j = 0; j < V; ++j) l[j] = src[j];
+      load_vec<V>(src, l);
       for (int p = 1; p < nparts; ++p) {
+        float q[V];
+        load_vec<V>(src + p * E, q);
 #pragma unroll
-        for (int j = 0; j < V; ++j) l[j] = l[j] + src[p * E + j];
+        for (int j = 0; j < V; ++j) l[j] = l[j] + q[j];
       }
-      if (lout) {
-#pragma unroll
-        for (int j = 0; j < V; ++j) lout[t * E + e0 + j] = l[j];
-      }
+      if (lout) store_vec<V>(lout + t * E + e0, l);
     } else {
 #pragma unroll
       for (int j = 0; j < V; ++j) l[j] = 0.0f;
@@ -202,7 +228,9 @@ __global__ __launch_bounds__(256) void topk_kernel(
   int my_id = 0;
   float my_sel = 0.0f, my_aux = 0.0f, m0 = 0.0f;
   float acc = 0.0f;  // sequential slot-order sum the weights divide by
-  for (int r = 0; r < k; ++r) {
+#pragma unroll
+  for (int r = 0; r < (KK > 0 ? KK : 8); ++r) {
+    if (KK == 0 && r >= k) break;
     float bv = sel[0], ba = aux[0];
     int bi = e0;
 #pragma unroll
@@ -267,9 +295,16 @@ static hipError_t launch_topk_ev(const float* logits, int nparts, const float* b
                                  float* w, int32_t* counts, hipStream_t s) {
   constexpr int TPB = 4 * (64 / (E / V));
   const dim3 grid((unsigned)((T + TPB - 1) / TPB));
-  hipLaunchKernelGGL((topk_kernel<E, V>), grid, dim3(256), 0, s, logits, nparts, bias, T, k,
-                     scoring, renorm, n_group, topk_group, route_scale, norm_min, lout, ids, w,
-                     counts);
+#define MOE_TOPK_ARGS                                                                      \
+  grid, dim3(256), 0, s, logits, nparts, bias, T, k, scoring, renorm, n_group, topk_group, \
+      route_scale, norm_min, lout, ids, w, counts
+  if (k == 8)
+    hipLaunchKernelGGL((topk_kernel<E, V, 8>), MOE_TOPK_ARGS);
+  else if (k == 2)
+    hipLaunchKernelGGL((topk_kernel<E, V, 2>), MOE_TOPK_ARGS);
+  else
+    hipLaunchKernelGGL((topk_kernel<E, V, 0>), MOE_TOPK_ARGS);
+#undef MOE_TOPK_ARGS
   return hipGetLastError();
 }
 
