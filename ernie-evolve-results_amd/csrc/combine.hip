@@ -61,12 +61,18 @@ __global__ __launch_bounds__(256) void combine_kernel(const u32x4* __restrict__ 
       r[j] = pair_row[(long long)t * K + j];
       wk[j] = w[(long long)t * K + j];
     }
+    // All k loads are unconditional so they issue back to back; a pair
+    // without a row (pair_row < 0) loads this thread's own output vector
+    // instead (valid memory) and the value is discarded by the select below.
     u32x4 yv[K];
 #pragma unroll
     for (int j = 0; j < K; ++j) {
-      yv[j] = (u32x4){0u, 0u, 0u, 0u};
-      if (r[j] >= 0) yv[j] = ld_nt(y + (long long)r[j] * nvec + v);
+      const u32x4* src = r[j] >= 0 ? y + (long long)r[j] * nvec + v : out + i;
+      yv[j] = ld_nt(src);
     }
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      if (r[j] < 0) yv[j] = (u32x4){0u, 0u, 0u, 0u};
     float acc[NE];
     if (shared) {
       VT::unpack(ld_nt(shared + i), acc);
@@ -115,13 +121,21 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const u32x4* __restri
       r[j] = __builtin_amdgcn_readfirstlane(pair_row[(long long)t * K + j]);
       wk[j] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(w[(long long)t * K + j])));
     }
+    // Unconditional loads (see combine_kernel): all VPW*k issue back to back.
     u32x4 yv[VPW][K];
 #pragma unroll
     for (int j = 0; j < K; ++j)
 #pragma unroll
-      for (int q = 0; q < VPW; ++q)
-        yv[q][j] = r[j] >= 0 ? ld_nt(y + (long long)r[j] * nvec + v0 + q * 64)
-                             : (u32x4){0u, 0u, 0u, 0u};
+      for (int q = 0; q < VPW; ++q) {
+        const u32x4* src = r[j] >= 0 ? y + (long long)r[j] * nvec + v0 + q * 64
+                                     : out + i0 + q * 64 + lane;
+        yv[q][j] = ld_nt(src);
+      }
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      if (r[j] < 0)
+#pragma unroll
+        for (int q = 0; q < VPW; ++q) yv[q][j] = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
     for (int q = 0; q < VPW; ++q) {
       float acc[NE];

@@ -26,12 +26,13 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
     const int v = i - t * nvec;
     const u32x4 val = ld_nt(x + i);
     const int* pr = pair_row + (long long)t * k;
+    // all k row indices first (one wait), then the k stores
+    int r[K > 0 ? K : 8];
 #pragma unroll
-    for (int j = 0; j < (K > 0 ? K : 8); ++j) {
-      if (K == 0 && j >= k) break;
-      const int r = pr[j];
-      if (r >= 0) st_nt(xg + (long long)r * nvec + v, val);
-    }
+    for (int j = 0; j < (K > 0 ? K : 8); ++j) r[j] = (K > 0 || j < k) ? pr[j] : -1;
+#pragma unroll
+    for (int j = 0; j < (K > 0 ? K : 8); ++j)
+      if (r[j] >= 0) st_nt(xg + (long long)r[j] * nvec + v, val);
   }
 }
 
