@@ -30,22 +30,44 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source of the library; returns the .so path."""
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC] + FLAGS + ["-I", os.path.join(REPO, "include"), "-I", CSRC]
-    # .cpp sources also hold HIP host code
-    cmd += ["-x", "hip"] + srcs + ["-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
-    out = "\n".join(l for l in res.stdout.splitlines()
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+
+
+def _finish(proc, what):
+    out, _ = proc.communicate()
+    out = "\n".join(l for l in out.splitlines()
                     if "packed-fp32-ops" not in l)  # host pass does not know the feature
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed (%d):\n%s" % (res.returncode, out))
-    if verbose and out.strip():
-        print(out)
+    if proc.returncode != 0:
+        raise RuntimeError("hipcc failed on %s (%d):\n%s" % (what, proc.returncode, out))
+    return out
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every HIP source of the library (in parallel), link the .so;
+    returns its path."""
+    objdir = os.path.join(HERE, "_obj")
+    os.makedirs(objdir, exist_ok=True)
+    inc = ["-I", os.path.join(REPO, "include"), "-I", CSRC]
+    compile_flags = [f for f in FLAGS if f != "-shared"]
+    procs, objs = [], []
+    for src in SOURCES:
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        objs.append(obj)
+        # .cpp sources also hold HIP host code
+        cmd = [HIPCC] + compile_flags + inc + ["-x", "hip", "-c", os.path.join(CSRC, src),
+                                               "-o", obj]
+        procs.append((_run(cmd, verbose), src))
+    logs = [_finish(p, src) for p, src in procs]
+    tmp = LIB_PATH + ".tmp"
+    link = _run([HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950"] + objs + ["-o", tmp], verbose)
+    logs.append(_finish(link, "link"))
+    if verbose:
+        for l in logs:
+            if l.strip():
+                print(l)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

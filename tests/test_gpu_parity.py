@@ -110,6 +110,28 @@ def test_route_fp32_weights_split(cuda):
     assert_weights(to_np(wts), ow)
 
 
+@pytest.mark.parametrize("T,E,k,scoring", [(1, 8, 1, 0), (333, 256, 8, 1), (4096, 32, 4, 2)])
+def test_route_fp32_weights_shapes(cuda, T, E, k, scoring):
+    """fp32 weights at other shapes: E=256 makes the split GEMM N=512 (two
+    256-column blocks); T=1 and T not a multiple of any tile."""
+    g = torch.Generator().manual_seed(T + E)
+    H = 1024
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = torch.randn(E, H, generator=g) * 0.02
+    b = torch.randn(E, generator=g) * 0.1
+    cfg = {0: RouteCfg(), 1: RouteCfg(M.SCORING_SIGMOID_GROUP, True, 8, 4, 2.5),
+           2: RouteCfg(M.SCORING_SOFTMAX_BIAS, True, 1, 1, 1.0, 1e-20)}[scoring]
+    logits, ids, wts, counts = M.route(x.to(cuda), w.to(cuda), b.to(cuda), k, cfg)
+    torch.cuda.synchronize()
+    ref = (x.double() @ w.double().t()).numpy()
+    s = (x.double().abs() @ w.double().abs().t()).numpy()
+    assert np.all(np.abs(to_np(logits) - ref) <= (2 * H * 2.0 ** -24 + 2.0 ** -16) * s)
+    oi, ow = O.score_topk(to_np(logits), b.numpy(), k, ocfg(cfg))
+    assert np.array_equal(to_np(ids), oi)
+    assert_weights(to_np(wts), ow)
+    assert np.array_equal(to_np(counts), np.bincount(oi.ravel(), minlength=E))
+
+
 # --------------------------------------------------------------------- stage 2
 TOPK_CASES = [
     ("C2-softmax-E8-k2", 8, 2, RouteCfg(), None),
@@ -244,7 +266,7 @@ def test_offsets_entry_point(cuda):
 
 
 # --------------------------------------------------------------------- stage 5
-@pytest.mark.parametrize("T,H,k", [(100, 256, 2), (64, 7168, 8), (33, 2048, 5)])
+@pytest.mark.parametrize("T,H,k", [(100, 256, 2), (64, 7168, 8), (33, 2048, 5), (1, 512, 1)])
 def test_combine_bf16(cuda, T, H, k):
     g = torch.Generator().manual_seed(H + k)
     y = torch.randn(T * k, H, generator=g).to(torch.bfloat16)
