@@ -143,6 +143,11 @@ TOPK_CASES = [
     ("sigmoid-group-E16-k2", 16, 2, RouteCfg(M.SCORING_SIGMOID_GROUP, True, 4, 2, 1.0), None),
     ("sigmoid-group-E128-k6", 128, 6, RouteCfg(M.SCORING_SIGMOID_GROUP, True, 8, 3, 2.5), "randn"),
     ("softmax-scaled-E256-k1", 256, 1, RouteCfg(M.SCORING_SOFTMAX, True, 1, 1, 1.5), None),
+    # small expert groups shrink the lanes' width: 32- and 64-lane token groups
+    # whose top reduction levels are xor shuffles instead of DPP row moves
+    ("sigmoid-group-E64-ng32-k3", 64, 3, RouteCfg(M.SCORING_SIGMOID_GROUP, True, 32, 5, 1.0), "randn"),
+    ("sigmoid-group-E256-ng64-k8", 256, 8, RouteCfg(M.SCORING_SIGMOID_GROUP, True, 64, 6, 2.5), "randn"),
+    ("sigmoid-group-E128-ng64-k2", 128, 2, RouteCfg(M.SCORING_SIGMOID_GROUP, False, 64, 2, 1.0), None),
 ]
 
 
