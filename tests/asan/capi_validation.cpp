@@ -1,0 +1,49 @@
+// Host-only driver for the C-ABI argument validation, built with
+// AddressSanitizer on the host pass (tests/test_capi_asan.py).  Every call
+// below must be rejected before anything is launched, so no GPU is needed.
+#include <cstdio>
+#include <cstring>
+
+#include "moe_route.h"
+
+static int failures = 0;
+#define EXPECT(call, code)                                                             \
+  do {                                                                                 \
+    int rc_ = (call);                                                                  \
+    if (rc_ != (code)) {                                                               \
+      std::printf("FAIL %s: got %d want %d (%s)\n", #call, rc_, code,                  \
+                  moe_last_error_string());                                            \
+      ++failures;                                                                      \
+    } else if (std::strlen(moe_last_error_string()) == 0 && (code) != 0) {             \
+      std::printf("FAIL %s: empty error string\n", #call);                            \
+      ++failures;                                                                      \
+    }                                                                                  \
+  } while (0)
+
+int main() {
+  void* fake = reinterpret_cast<void*>(0x10000);
+  moe_route_cfg cfg{MOE_SCORING_SIGMOID_GROUP, 1, 8, 4, 2.5f, 0.0f};
+  int32_t* ip = static_cast<int32_t*>(fake);
+  float* fp = static_cast<float*>(fake);
+  EXPECT(moe_route(fake, fake, 0, fp, 16, 100, 256, 8, &cfg, fp, ip, fp, nullptr, nullptr, 0, nullptr), MOE_ERR_UNSUPPORTED);
+  EXPECT(moe_route(fake, fake, 0, fp, 16, 128, 12, 8, &cfg, fp, ip, fp, nullptr, nullptr, 0, nullptr), MOE_ERR_UNSUPPORTED);
+  EXPECT(moe_route(fake, fake, 1, fp, 16, 128, 256, 8, &cfg, fp, ip, fp, nullptr, nullptr, 0, nullptr), MOE_ERR_WORKSPACE);
+  EXPECT(moe_route(nullptr, fake, 0, fp, 16, 128, 256, 8, &cfg, fp, ip, fp, nullptr, nullptr, 0, nullptr), MOE_ERR_NULL_POINTER);
+  EXPECT(moe_route(fake, fake, 0, fp, 16, 128, 256, 8, nullptr, fp, ip, fp, nullptr, nullptr, 0, nullptr), MOE_ERR_NULL_POINTER);
+  cfg.n_group = 6;
+  EXPECT(moe_topk(fp, nullptr, 4, 256, 8, &cfg, ip, fp, nullptr, nullptr), MOE_ERR_INVALID_ARG);
+  cfg.n_group = 128;
+  EXPECT(moe_topk(fp, nullptr, 4, 256, 8, &cfg, ip, fp, nullptr, nullptr), MOE_ERR_UNSUPPORTED);
+  EXPECT(moe_permute(fake, 0, ip, 8, 256, 16, 9, 0, fake, nullptr, ip, ip, nullptr, nullptr, fake, 1 << 20, nullptr), MOE_ERR_INVALID_ARG);
+  EXPECT(moe_permute(fake, 0, ip, 8, 192, 16, 2, 2, fake, fp, ip, ip, nullptr, nullptr, fake, 1 << 20, nullptr), MOE_ERR_UNSUPPORTED);
+  EXPECT(moe_permute(fake, 0, ip, 8, 256, 16, 2, 0, fake, nullptr, ip, ip, nullptr, nullptr, fake, 8, nullptr), MOE_ERR_WORKSPACE);
+  EXPECT(moe_combine(fake, 0, ip, fp, nullptr, 4, 4, 2, fake, nullptr), MOE_ERR_ALIGNMENT);
+  EXPECT(moe_combine(nullptr, 0, nullptr, nullptr, nullptr, 0, 64, 2, nullptr, nullptr), MOE_OK);
+  EXPECT(moe_offsets(ip, 2000, ip, nullptr), MOE_ERR_INVALID_ARG);
+  EXPECT(moe_router_gemm(fake, fake, 4, 96, 8, fp, nullptr), MOE_ERR_UNSUPPORTED);
+  if (moe_route_workspace_bytes(32768, 7168, 256, MOE_DTYPE_BF16) != (size_t)32768 * 2 * 256 * 4) ++failures;
+  if (moe_permute_workspace_bytes(32768, 256, 8) != (size_t)256 * 1024 * 4 + 1024) ++failures;
+  if (moe_version() != MOE_ROUTE_VERSION) ++failures;
+  std::printf("%s (%d failures)\n", failures ? "FAILED" : "OK", failures);
+  return failures ? 1 : 0;
+}
