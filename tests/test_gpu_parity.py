@@ -183,6 +183,34 @@ def test_topk_tie_stress_fixture(cuda, name):
     assert_weights(to_np(wts), d["weights"])
 
 
+def test_sigmoid_weights_bit_exact_wide_sweep(cuda):
+    """Sigmoid scoring without renormalisation at unit scale outputs the
+    sigmoid itself, so every weight must equal the oracle's det_sigmoid of
+    its expert's logit bit for bit.  8M logits: random fp32 bit patterns with
+    |x| <= 90 (both clamps and the whole exp range), a dense ramp through
+    [-20, 20], and the clamp edges."""
+    g = np.random.default_rng(5)
+    n = 1 << 23
+    mag = g.integers(0, 0x42B40000, size=n, dtype=np.uint32)  # |x| <= 90
+    vals = (mag | (g.integers(0, 2, size=n, dtype=np.uint32) << 31)).view(np.float32)
+    vals[: 1 << 20] = np.linspace(-20, 20, 1 << 20, dtype=np.float32)
+    edges = np.array([-90, -86.5, -86, -85.99999, 0, 85.99999, 86, 86.5, 90, -0.0, 1e-30, -1e-30],
+                     dtype=np.float32)
+    vals[1 << 20: (1 << 20) + edges.size] = edges
+    logits = torch.from_numpy(vals.reshape(-1, 8).copy())
+    cfg = RouteCfg(M.SCORING_SIGMOID_GROUP, False, 1, 1, 1.0)
+    ids, wts, _ = M.topk(logits.to(cuda), None, 8, cfg)
+    torch.cuda.synchronize()
+    ids_np = to_np(ids)
+    picked = np.take_along_axis(logits.numpy(), ids_np.astype(np.int64), axis=1)
+    want = O.det_sigmoid(picked)
+    assert np.array_equal(to_np(wts).view(np.uint32), want.view(np.uint32))
+    # and the ranking itself on a sample of rows
+    rows = slice(0, 4096)
+    oi, _ = O.score_topk(logits.numpy()[rows], None, 8, ocfg(cfg))
+    assert np.array_equal(ids_np[rows], oi)
+
+
 # --------------------------------------------------------------------- stages 3-4
 def check_permutation(p, ids_np, E):
     rt, pr = O.permutation(ids_np)
