@@ -1,0 +1,249 @@
+// Expert grouped GEMM over the expert-contiguous rows the permute produces.
+//
+// Replaces the reference's CUTLASS grouped GEMMs (moe_gemm.h:66-95,
+// moe_gemm.cu:616-650): group g owns rows [offs[g-1], offs[g]) of a
+// (offs = inclusive group ends, offs[-1] = 0 -- exactly `offsets + 1` of
+// moe_permute) and
+//   plain : out[r, :] = a[r, :] . w[g]^T                     (grouped_mm)
+//   swiglu: h[r, :]   = silu(a[r, :] . wg[g]^T) * (a[r, :] . wu[g]^T)
+//           (grouped_mm_pair followed by silu*mul, fused into the epilogue)
+// with a [M, K] bf16, w [G, N, K] bf16 (both K-contiguous), fp32 accumulate.
+//
+// Plan (the reference's plan_kernel builds per-group pointers for CUTLASS on
+// the device; here it is one scan): tile_start[g] = sum over g' < g of
+// ceil(m_g' / 256), on the device, so nothing waits for the host.  The grid
+// is sized by the bound sum ceil(m_g / 256) <= ceil(M / 256) + G; blocks past
+// the last tile return at once.
+//
+// Tiles: 256 rows x 256 weight rows, 64-wide K steps, staged in LDS by the
+// gfx950 global_load_lds DMA into a 2-stage ring with an XOR-swizzled 16-byte
+// chunk layout, 16 waves with 64 x 64 accumulators of
+// v_mfma_f32_16x16x32_bf16 (the router GEMM's pipeline).  Block ids are
+// remapped so that the n-tiles of one row tile run on one XCD: consecutive
+// logical tiles share the A rows, which then stay in that XCD's L2, while
+// every weight tile is read from HBM once per row tile.
+//
+// swiglu interleaves the two weights at 16-row granularity inside the B
+// tile (rows 16f..16f+15 come from wg for even f, from wu for odd f), so the
+// gate and up accumulators of the same output columns sit in one wave and
+// the epilogue forms h without an exchange.  A tile then covers 128 output
+// columns.
+//
+// Identity shortcut (the reference's ident_a / ident_m): a group whose row
+// count equals ident_m takes its A rows from ident_a (row i of the group =
+// row i of ident_a) instead of a.
+#include "moe_common.h"
+
+namespace moe {
+
+constexpr int kGgBM = 256, kGgBN = 256, kGgBK = 64;
+
+// One workgroup of 1024 threads: inclusive scan of per-group tile counts.
+__global__ __launch_bounds__(1024) void gg_plan_kernel(const int* __restrict__ offs, int G, int M,
+                                                       int* __restrict__ tile_start) {
+  __shared__ int part[16];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int base = 0; base < G; base += 1024) {
+    const int g = base + threadIdx.x;
+    int tiles = 0;
+    if (g < G) {
+      const int lo = g > 0 ? min(max(offs[g - 1], 0), M) : 0;
+      const int hi = min(max(offs[g], 0), M);
+      tiles = hi > lo ? (hi - lo + kGgBM - 1) / kGgBM : 0;
+    }
+    // wave inclusive scan
+    int v = tiles;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(v, o, 64);
+      if (lane >= o) v += u;
+    }
+    if (lane == 63) part[wave] = v;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      int p = part[threadIdx.x];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const int u = __shfl_up(p, o, 16);
+        if ((threadIdx.x & 15) >= o) p += u;
+      }
+      part[threadIdx.x] = p;  // inclusive over waves
+    }
+    __syncthreads();
+    const int incl = carry + (wave > 0 ? part[wave - 1] : 0) + v;
+    if (g < G) tile_start[g + 1] = incl;
+    if (g == 0) tile_start[0] = 0;
+    __syncthreads();
+    if (threadIdx.x == 1023) carry = incl;
+    __syncthreads();
+  }
+  if (G == 0 && threadIdx.x == 0) tile_start[0] = 0;
+}
+
+// silu(g) * u in fp32
+__device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(1024) void grouped_gemm_kernel(
+    const __bf16* __restrict__ a, const __bf16* __restrict__ ident_a, int ident_m,
+    const __bf16* __restrict__ w0, const __bf16* __restrict__ w1,
+    const int* __restrict__ offs, const int* __restrict__ tile_start, int G, int M, int N, int K,
+    int n_tiles, unsigned short* __restrict__ out) {
+  constexpr int BM = kGgBM, BN = kGgBN, BK = kGgBK, NS = 2, CH = 8, ROWB = 128, RPI = 8;
+  constexpr int STAGE_B = (BM + BN) * ROWB;
+  constexpr int A_INST = BM / RPI, B_INST = BN / RPI, NW = 16, PER_WAVE = (A_INST + B_INST) / NW;
+  constexpr int WM = 4, WN = 4, WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B];
+
+  // XCD-aware order: gridDim.x is a multiple of 8, hardware block b runs on
+  // XCD b % 8; logical tiles [x*nb/8, (x+1)*nb/8) all run on XCD x.
+  const unsigned nb = gridDim.x, b = blockIdx.x;
+  const unsigned l = (b & 7u) * (nb >> 3) + (b >> 3);
+  const int mt = (int)(l / (unsigned)n_tiles), nt = (int)(l % (unsigned)n_tiles);
+  if (mt >= tile_start[G]) return;
+  // group of this row tile: the last g with tile_start[g] <= mt
+  int lo = 0, hi = G - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tile_start[mid] <= mt) lo = mid; else hi = mid - 1;
+  }
+  const int g = lo;
+  const int gs = g > 0 ? min(max(offs[g - 1], 0), M) : 0;
+  const int ge = min(max(offs[g], 0), M);
+  const int r0 = gs + (mt - tile_start[g]) * BM;   // first row of the tile
+  const int rlast = ge - 1;                        // last row of the group
+  const bool ident = ident_m > 0 && ge - gs == ident_m;
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  auto swz = [](int r) { return (r >> 1) & (CH - 1); };
+  const long long wbase = (long long)g * N * K;
+
+  const __bf16* src[PER_WAVE];
+#pragma unroll
+  for (int q = 0; q < PER_WAVE; ++q) {
+    const int gi = wave * PER_WAVE + q;
+    const int p = lane % CH;
+    if (gi < A_INST) {
+      const int r = gi * RPI + lane / CH;
+      const int row = min(r0 + r, rlast);  // rows past the group are loaded, never stored
+      const __bf16* arow = ident ? ident_a + (long long)(row - gs) * K : a + (long long)row * K;
+      src[q] = arow + (p ^ swz(r)) * 8;
+    } else {
+      const int r = (gi - A_INST) * RPI + lane / CH;
+      int wrow;
+      const __bf16* wsrc = w0;
+      if (SWIGLU) {
+        const int f = r >> 4;
+        wrow = nt * (BN / 2) + (f >> 1) * 16 + (r & 15);
+        if (f & 1) wsrc = w1;
+      } else {
+        wrow = nt * BN + r;
+      }
+      wrow = min(wrow, N - 1);
+      src[q] = wsrc + wbase + (long long)wrow * K + (p ^ swz(r)) * 8;
+    }
+  }
+  auto issue = [&](int kt, int st) {
+#pragma unroll
+    for (int q = 0; q < PER_WAVE; ++q) {
+      auto* dst = (__attribute__((address_space(3))) void*)(lds + st * STAGE_B +
+                                                            (wave * PER_WAVE + q) * 1024);
+      __builtin_amdgcn_global_load_lds((const void*)(src[q] + kt * BK), dst, 16, 0, 0);
+    }
+  };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  const int KT = K / BK;
+  issue(0, 0);
+  const int fr = lane & 15, fc = lane >> 4;
+  for (int kt = 0; kt < KT; ++kt) {
+    // stage kt landed (this wave's DMA), then the barrier publishes every
+    // wave's DMA and retires all reads of the buffer reloaded next
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + 1 < KT) issue(kt + 1, (kt + 1) & 1);
+    const char* sb = lds + (kt & 1) * STAGE_B;
+#pragma unroll
+    for (int kk = 0; kk < BK / 32; ++kk) {
+      bf16x8 av[FM], bv[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * WTM + i * 16 + fr, c = kk * 4 + fc;
+        av[i] = *reinterpret_cast<const bf16x8*>(sb + r * ROWB + ((c ^ swz(r)) * 16));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int r = wn * WTN + j * 16 + fr, c = kk * 4 + fc;
+        bv[j] = *reinterpret_cast<const bf16x8*>(sb + BM * ROWB + r * ROWB + ((c ^ swz(r)) * 16));
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Epilogue: lane holds rows (lane>>4)*4 + r, column lane & 15 of each 16x16 tile.
+  const int ldo = N;
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = r0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
+      if (row > rlast) continue;
+      unsigned short* orow = out + (long long)row * ldo;
+      if (SWIGLU) {
+#pragma unroll
+        for (int j = 0; j < FN; j += 2) {
+          const int col = nt * (BN / 2) + (wn * FN + j) / 2 * 16 + (lane & 15);
+          if (col < N) orow[col] = (unsigned short)f2bf(swiglu(acc[i][j][r], acc[i][j + 1][r]));
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int col = nt * BN + wn * WTN + j * 16 + (lane & 15);
+          if (col < N) orow[col] = (unsigned short)f2bf(acc[i][j][r]);
+        }
+      }
+    }
+}
+
+int grouped_gemm_n_tiles(int N, bool swiglu) {
+  const int per = swiglu ? kGgBN / 2 : kGgBN;
+  return (N + per - 1) / per;
+}
+
+// tile_start: [G+1] ints of workspace.  offs: inclusive group ends (device).
+hipError_t launch_grouped_gemm(const void* a, const void* ident_a, int ident_m, const void* w0,
+                               const void* w1, const int32_t* offs, int G, int M, int N, int K,
+                               bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
+  hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, tile_start);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (M == 0 || N == 0 || G == 0) return hipSuccess;
+  const int n_tiles = grouped_gemm_n_tiles(N, swiglu);
+  const long long m_bound = ((long long)M + kGgBM - 1) / kGgBM + G;
+  long long blocks = m_bound * n_tiles;
+  blocks = (blocks + 7) / 8 * 8;
+  const dim3 grid((unsigned)blocks), blk(1024);
+  if (swiglu)
+    hipLaunchKernelGGL(grouped_gemm_kernel<true>, grid, blk, 0, s, (const __bf16*)a,
+                       (const __bf16*)ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1,
+                       offs, tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
+  else
+    hipLaunchKernelGGL(grouped_gemm_kernel<false>, grid, blk, 0, s, (const __bf16*)a,
+                       (const __bf16*)ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0,
+                       offs, tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
+  return hipGetLastError();
+}
+
+}  // namespace moe

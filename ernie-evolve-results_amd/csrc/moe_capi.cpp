@@ -266,4 +266,51 @@ int moe_combine(const void* y, int y_dtype, const int32_t* pair_row, const float
                   "combine");
 }
 
+size_t moe_grouped_gemm_workspace_bytes(int G) {
+  if (G < 0) return 0;
+  return round256((size_t)(G + 1) * 4);
+}
+
+static int grouped_common(const void* a, const void* w0, const void* w1, const int32_t* offs,
+                          int G, int M, int N, int K, const void* ident_a, int ident_m,
+                          void* out, void* ws, size_t ws_bytes, void* stream, bool swiglu) {
+  if (G < 1 || G > 65536) return fail(MOE_ERR_INVALID_ARG, "G=%d not in [1, 65536]", G);
+  if (M < 0 || N < 1 || K < 1) return fail(MOE_ERR_INVALID_ARG, "M=%d, N=%d, K=%d", M, N, K);
+  if (K % 64 != 0) return fail(MOE_ERR_UNSUPPORTED, "K=%d is not a multiple of 64", K);
+  if (ident_m < 0) return fail(MOE_ERR_INVALID_ARG, "ident_m=%d < 0", ident_m);
+  if (!offs || !ws) return fail(MOE_ERR_NULL_POINTER, "offs and ws are required");
+  if (M > 0 && (!a || !w0 || !w1 || !out))
+    return fail(MOE_ERR_NULL_POINTER, "a, the weights and the output are required");
+  if (ident_m > 0 && !ident_a) return fail(MOE_ERR_NULL_POINTER, "ident_m > 0 needs ident_a");
+  if ((a && !aligned16(a)) || (w0 && !aligned16(w0)) || (w1 && !aligned16(w1)) ||
+      (ident_a && !aligned16(ident_a)))
+    return fail(MOE_ERR_ALIGNMENT, "a, ident_a and the weights must be 16-byte aligned");
+  if ((long long)M * K >= (1ll << 40) || (long long)G * N * K >= (1ll << 40))
+    return fail(MOE_ERR_UNSUPPORTED, "operands too large");
+  const size_t need = moe_grouped_gemm_workspace_bytes(G);
+  if (ws_bytes < need)
+    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws_bytes, need);
+  if (!aligned16(ws)) return fail(MOE_ERR_ALIGNMENT, "workspace not 16-byte aligned");
+  const long long blocks = (((long long)M + 255) / 256 + G) *
+                           moe::grouped_gemm_n_tiles(N, swiglu);
+  if (blocks >= (1ll << 31)) return fail(MOE_ERR_UNSUPPORTED, "too many tiles (%lld)", blocks);
+  return launched(moe::launch_grouped_gemm(a, ident_a, ident_m, w0, w1, offs, G, M, N, K, swiglu,
+                                           out, (int32_t*)ws, (hipStream_t)stream),
+                  swiglu ? "grouped_swiglu" : "grouped_gemm");
+}
+
+int moe_grouped_gemm(const void* a, const void* w, const int32_t* offs, int G, int M, int N,
+                     int K, const void* ident_a, int ident_m, void* out, void* ws,
+                     size_t ws_bytes, void* stream) {
+  return grouped_common(a, w, w, offs, G, M, N, K, ident_a, ident_m, out, ws, ws_bytes, stream,
+                        false);
+}
+
+int moe_grouped_swiglu(const void* a, const void* wg, const void* wu, const int32_t* offs,
+                       int G, int M, int N, int K, const void* ident_a, int ident_m, void* h,
+                       void* ws, size_t ws_bytes, void* stream) {
+  return grouped_common(a, wg, wu, offs, G, M, N, K, ident_a, ident_m, h, ws, ws_bytes, stream,
+                        true);
+}
+
 }  // extern "C"

@@ -58,6 +58,13 @@ hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, int T, int 
 hipError_t launch_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* w,
                           const void* shared, int T, int H, int k, void* out, hipStream_t s);
 
+// Column tiles of the grouped GEMM for N output columns.
+int grouped_gemm_n_tiles(int N, bool swiglu);
+// Expert grouped GEMM (plain or SwiGLU epilogue); tile_start is [G+1] ints of workspace.
+hipError_t launch_grouped_gemm(const void* a, const void* ident_a, int ident_m, const void* w0,
+                               const void* w1, const int32_t* offs, int G, int M, int N, int K,
+                               bool swiglu, void* out, int32_t* tile_start, hipStream_t s);
+
 // Experts per lane of the scoring kernel for (E, scoring, n_group).
 int topk_lane_width(int E, int scoring, int n_group);
 

@@ -30,7 +30,8 @@ ERR_NAMES = {-1: "MOE_ERR_NULL_POINTER", -2: "MOE_ERR_INVALID_ARG", -3: "MOE_ERR
 # Every extern "C" symbol of include/moe_route.h.
 EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
            "moe_router_gemm", "moe_topk", "moe_route", "moe_offsets",
-           "moe_permute_workspace_bytes", "moe_permute", "moe_combine"]
+           "moe_permute_workspace_bytes", "moe_permute", "moe_combine",
+           "moe_grouped_gemm_workspace_bytes", "moe_grouped_gemm", "moe_grouped_swiglu"]
 
 
 class MoeError(RuntimeError):
@@ -82,6 +83,12 @@ def lib():
                                   _P]
         L.moe_combine.restype = _I
         L.moe_combine.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]
+        L.moe_grouped_gemm_workspace_bytes.restype = _Z
+        L.moe_grouped_gemm_workspace_bytes.argtypes = [_I]
+        L.moe_grouped_gemm.restype = _I
+        L.moe_grouped_gemm.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _Z, _P]
+        L.moe_grouped_swiglu.restype = _I
+        L.moe_grouped_swiglu.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _Z, _P]
         _lib = L
     return _lib
 
@@ -233,6 +240,52 @@ def combine(y, pair_row, topk_w, shared=None, out=None):
     return out
 
 
+def _grouped_args(a, offs, ident_a, ident_m):
+    _dev(a, "a")
+    _dev(offs, "offs")
+    if offs.dtype != torch.int32:
+        raise RuntimeError("offs must be int32 inclusive group ends")
+    if a.dtype != torch.bfloat16:
+        raise RuntimeError("a must be bf16")
+    if ident_m and ident_a is None:
+        raise RuntimeError("ident_m > 0 needs ident_a")
+    ws = torch.empty(max(lib().moe_grouped_gemm_workspace_bytes(offs.numel()), 256),
+                     dtype=torch.uint8, device=a.device)
+    return ws
+
+
+def grouped_gemm(a, w, offs, ident_a=None, ident_m=0, out=None):
+    """Expert grouped GEMM (the reference's grouped_mm, moe_gemm.h:66-85):
+    out[r] = a[r] . w[g]^T for the rows r of group g = [offs[g-1], offs[g]).
+    a [M,K] bf16, w [G,N,K] bf16, offs [G] int32 INCLUSIVE ends (moe_permute's
+    offsets[1:]); returns out [M,N] bf16.  Rows outside every group are not
+    written."""
+    ws = _grouped_args(a, offs, ident_a, ident_m)
+    G, N, K = w.shape
+    M = a.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    _check(lib().moe_grouped_gemm(_ptr(a), _ptr(w), _ptr(offs), G, M, N, K, _ptr(ident_a),
+                                  int(ident_m), _ptr(out), _ptr(ws), ws.numel(), _stream(a)))
+    return out
+
+
+def grouped_swiglu(a, wg, wu, offs, ident_a=None, ident_m=0, out=None):
+    """SwiGLU expert projection (grouped_mm_pair, moe_gemm.h:87-95, plus the
+    silu*mul): h[r] = silu(a[r] . wg[g]^T) * (a[r] . wu[g]^T), bf16 [M,N]."""
+    ws = _grouped_args(a, offs, ident_a, ident_m)
+    if wg.shape != wu.shape:
+        raise RuntimeError("gate and up weights must have one shape")
+    G, N, K = wg.shape
+    M = a.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    _check(lib().moe_grouped_swiglu(_ptr(a), _ptr(wg), _ptr(wu), _ptr(offs), G, M, N, K,
+                                    _ptr(ident_a), int(ident_m), _ptr(out), _ptr(ws), ws.numel(),
+                                    _stream(a)))
+    return out
+
+
 def route_dispatch_combine(x, w, bias, y, k, cfg: RouteCfg, fp8=False):
     """The whole path for one batch: route, permute (bf16 or fp8), combine y."""
     logits, ids, wts, counts = route(x, w, bias, k, cfg)
@@ -253,10 +306,16 @@ def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, e
     """Drop-in for the reference's run() (K:4067-4077): returns
     (out [B,S,H] bf16, router_logits [T,64] fp32).
 
-    Routing (fp32 gate_weight hi/lo split, softmax + post-softmax bias, top-8,
-    w = c / max(sum c, norm_min)), dispatch and combine run in libmoe_route.
-    The expert SwiGLU MLPs, which the reference runs as CUTLASS grouped GEMMs,
-    are plain torch matmuls over each expert's contiguous row range here."""
+    Every stage runs in libmoe_route, enqueued on the current stream with no
+    host synchronisation:
+      routing   fp32 gate_weight hi/lo split, softmax + post-softmax bias,
+                top-8, w = c / max(sum c, norm_min)  (K:1786-1920);
+      dispatch  stable expert-major permutation + row gather (K:1922-2238);
+      experts   h = silu(xg . Wg[e]^T) * (xg . Wu[e]^T), y = h . Wd[e]^T as two
+                grouped GEMMs over the device offsets (the reference's CUTLASS
+                grouped GEMMs, moe_gemm.h:66-95);
+      shared    the same two kernels with one group of all T rows;
+      combine   out = shared + sum_j w_j y[pair_row]  (K:2365-2428)."""
     B, S, H = hidden_states.shape
     T = B * S
     x = hidden_states.reshape(T, H)
@@ -266,19 +325,14 @@ def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, e
     logits, ids, wts, _ = route(x, gate_weight.float().contiguous(),
                                 e_score_correction_bias.float().contiguous(), REF_TOPK, cfg)
     p = permute(x, ids, E)
-    offs = p["offsets"].cpu().tolist()
-    xg = p["xg"]
-    y = torch.empty_like(xg)
-    silu = torch.nn.functional.silu
-    for e in range(E):
-        a, b = offs[e], offs[e + 1]
-        if a == b:
-            continue
-        xe = xg[a:b]
-        h = silu(xe @ expert_gate_proj[e].t()) * (xe @ expert_up_proj[e].t())
-        y[a:b] = h @ expert_down_proj[e].t()
-    sh = (silu(x @ shared_gate_proj.t()) * (x @ shared_up_proj.t())) @ shared_down_proj.t()
-    out = combine(y, p["pair_row"], wts, shared=sh.contiguous())
+    ends = p["offsets"][1:]  # inclusive group ends (moe_gemm.h:66-69)
+    h = grouped_swiglu(p["xg"], expert_gate_proj.contiguous(), expert_up_proj.contiguous(), ends)
+    y = grouped_gemm(h, expert_down_proj.contiguous(), ends)
+    dense = torch.full((1,), T, dtype=torch.int32, device=x.device)
+    sh_h = grouped_swiglu(x.contiguous(), shared_gate_proj.contiguous().unsqueeze(0),
+                          shared_up_proj.contiguous().unsqueeze(0), dense)
+    sh = grouped_gemm(sh_h, shared_down_proj.contiguous().unsqueeze(0), dense)
+    out = combine(y, p["pair_row"], wts, shared=sh)
     return out.view(B, S, H), logits
 
 

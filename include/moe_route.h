@@ -136,6 +136,35 @@ int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int 
 int moe_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* topk_w,
                 const void* shared, int T, int H, int k, void* out, void* stream);
 
+/* Workspace bytes moe_grouped_gemm / moe_grouped_swiglu need: the device
+ * tile plan, (G+1) int32. */
+size_t moe_grouped_gemm_workspace_bytes(int G);
+
+/* Expert grouped GEMM over expert-contiguous rows.  Replaces grouped_mm
+ * (moe_gemm.h:66-85) and its device plan (plan_kernel, moe_gemm.cu:616-650):
+ *   out[r, :] = a[r, :] . w[g]^T  for every row r of group g,
+ * group g = rows [offs[g-1], offs[g]) (offs[-1] = 0): offs[G] int32 are the
+ * INCLUSIVE group ends on the device -- moe_permute's `offsets + 1`.
+ *   a   [M, K] bf16 row-major;  w [G, N, K] bf16 (K-contiguous, the
+ *       reference's expert_*_proj layout);  out [M, N] bf16.
+ *   ident_a / ident_m: identity shortcut (moe_gemm.h:72-77): a group with
+ *       exactly ident_m rows reads row i from ident_a [ident_m, K] instead of
+ *       a.  ident_m = 0 disables it (ident_a may then be NULL).
+ * fp32 accumulation on MFMA.  offs must be non-decreasing and <= M; values
+ * outside [0, M] are clamped, never dereferenced.  Needs K % 64 == 0, N >= 1. */
+int moe_grouped_gemm(const void* a, const void* w, const int32_t* offs, int G, int M, int N,
+                     int K, const void* ident_a, int ident_m, void* out, void* ws,
+                     size_t ws_bytes, void* stream);
+
+/* SwiGLU expert projection: grouped_mm_pair (moe_gemm.h:87-95) with the
+ * silu*mul of the gate and up outputs fused into the epilogue (the
+ * reference's int8 gate+up GEMM emits h itself, kernel.cu:61-62):
+ *   h[r, :] = silu(a[r, :] . wg[g]^T) * (a[r, :] . wu[g]^T)
+ * wg, wu [G, N, K] bf16; h [M, N] bf16; the rest as moe_grouped_gemm. */
+int moe_grouped_swiglu(const void* a, const void* wg, const void* wu, const int32_t* offs,
+                       int G, int M, int N, int K, const void* ident_a, int ident_m, void* h,
+                       void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

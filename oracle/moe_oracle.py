@@ -19,6 +19,9 @@ configurations name:
 * dispatch permutation    K:2109-2189 (dispatch_body: inv[s]=pos, tok[pos]=t)
 * gather                  K:2216-2230 (gather_body)
 * combine                 K:2365-2428 (combine_kernel: acc = shared, acc += w*y)
+* expert grouped GEMM     moe_gemm.h:66-95, moe_gemm.cu:616-650 (grouped_mm /
+                          grouped_mm_pair over inclusive group ends offs; the
+                          SwiGLU h = silu(g) * u of the expert MLP)
 
 Two deliberate differences from the reference, shared by the HIP kernels:
 
@@ -316,6 +319,57 @@ def combine(y, pair_row, topk_w, shared=None, out_dtype=None):
     for j in range(k):
         acc = acc + w[:, j:j + 1] * yt[rows[:, j]].float()
     return acc.to(out_dtype or yt.dtype)
+
+
+# ---------------------------------------------------------------------------
+# expert grouped GEMM (the consumer of the offsets)
+# ---------------------------------------------------------------------------
+def group_bounds(offs_incl, M):
+    """[(start, end)] row range of each group from inclusive ends offs
+    (moe_gemm.h:66-69: group g owns rows [offs[g-1], offs[g]), offs[-1] = 0),
+    clamped into [0, M] as the device plan does."""
+    out, prev = [], 0
+    for e in np.asarray(offs_incl, dtype=np.int64).tolist():
+        lo = min(max(prev, 0), M)
+        hi = min(max(e, 0), M)
+        out.append((lo, max(lo, hi)))
+        prev = e
+    return out
+
+
+def _group_a(a, lo, hi, ident_a, ident_m):
+    """A rows of one group; the identity shortcut (moe_gemm.h:72-77) takes a
+    group with exactly ident_m rows from ident_a instead."""
+    if ident_m and hi - lo == ident_m:
+        return torch.as_tensor(ident_a)[:ident_m].float()
+    return torch.as_tensor(a)[lo:hi].float()
+
+
+def grouped_gemm(a, w, offs_incl, ident_a=None, ident_m=0):
+    """out[r] = a[r] . w[g]^T for the rows r of group g (grouped_mm,
+    moe_gemm.h:66-85), fp32 accumulate, fp32 result.  Rows outside every group
+    are left 0."""
+    at = torch.as_tensor(a)
+    wt = torch.as_tensor(w)
+    M = at.shape[0]
+    out = torch.zeros(M, wt.shape[1], dtype=torch.float32)
+    for g, (lo, hi) in enumerate(group_bounds(offs_incl, M)):
+        if hi > lo:
+            out[lo:hi] = _group_a(at, lo, hi, ident_a, ident_m) @ wt[g].float().t()
+    return out
+
+
+def silu(v):
+    """silu(v) = v / (1 + exp(-v)) in fp32 (torch's fp32 silu)."""
+    return torch.nn.functional.silu(torch.as_tensor(v).float())
+
+
+def grouped_swiglu(a, wg, wu, offs_incl, ident_a=None, ident_m=0):
+    """h[r] = silu(a[r] . wg[g]^T) * (a[r] . wu[g]^T): grouped_mm_pair
+    (moe_gemm.h:87-95) followed by the expert MLP's silu*mul, fp32 result."""
+    g = grouped_gemm(a, wg, offs_incl, ident_a, ident_m)
+    u = grouped_gemm(a, wu, offs_incl, ident_a, ident_m)
+    return silu(g) * u
 
 
 # ---------------------------------------------------------------------------

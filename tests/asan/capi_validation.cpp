@@ -41,6 +41,12 @@ int main() {
   EXPECT(moe_combine(nullptr, 0, nullptr, nullptr, nullptr, 0, 64, 2, nullptr, nullptr), MOE_OK);
   EXPECT(moe_offsets(ip, 2000, ip, nullptr), MOE_ERR_INVALID_ARG);
   EXPECT(moe_router_gemm(fake, fake, 4, 96, 8, fp, nullptr), MOE_ERR_UNSUPPORTED);
+  EXPECT(moe_grouped_gemm(fake, fake, ip, 0, 64, 128, 256, nullptr, 0, fake, fake, 4096, nullptr), MOE_ERR_INVALID_ARG);
+  EXPECT(moe_grouped_gemm(fake, fake, ip, 4, 64, 128, 100, nullptr, 0, fake, fake, 4096, nullptr), MOE_ERR_UNSUPPORTED);
+  EXPECT(moe_grouped_gemm(fake, fake, ip, 4, 64, 128, 256, nullptr, 3, fake, fake, 4096, nullptr), MOE_ERR_NULL_POINTER);
+  EXPECT(moe_grouped_gemm(fake, fake, ip, 4, 64, 128, 256, nullptr, 0, fake, fake, 8, nullptr), MOE_ERR_WORKSPACE);
+  EXPECT(moe_grouped_swiglu(fake, fake, nullptr, ip, 4, 64, 128, 256, nullptr, 0, fake, fake, 4096, nullptr), MOE_ERR_NULL_POINTER);
+  if (moe_grouped_gemm_workspace_bytes(64) != 512) ++failures;
   if (moe_route_workspace_bytes(32768, 7168, 256, MOE_DTYPE_BF16) != (size_t)32768 * 2 * 256 * 4) ++failures;
   if (moe_permute_workspace_bytes(32768, 256, 8) != (size_t)256 * 1024 * 4 + 1024) ++failures;
   if (moe_version() != MOE_ROUTE_VERSION) ++failures;

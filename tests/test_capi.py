@@ -119,6 +119,27 @@ def test_workspace_sizes():
     assert L.moe_permute_workspace_bytes(32768, 256, 8) == 256 * 1024 * 4 + 1024
 
 
+def test_grouped_gemm_validation():
+    L = M.lib()
+    ws = ctypes.c_void_p(0x10000)
+    args = lambda G=4, Mr=64, N=128, K=256, im=0, ia=None, wsb=4096, a=FAKE: (
+        a, FAKE, FAKE, G, Mr, N, K, ia, im, FAKE, ws, wsb, None)
+    err(L.moe_grouped_gemm(*args(G=0)), -2, "G=0")
+    err(L.moe_grouped_gemm(*args(K=100)), -3, "multiple of 64")
+    err(L.moe_grouped_gemm(*args(N=0)), -2)
+    err(L.moe_grouped_gemm(*args(Mr=-1)), -2)
+    err(L.moe_grouped_gemm(*args(im=-2)), -2, "ident_m")
+    err(L.moe_grouped_gemm(*args(im=5)), -1, "ident_a")
+    err(L.moe_grouped_gemm(*args(a=None)), -1)
+    err(L.moe_grouped_gemm(*args(wsb=4)), -4, "workspace")
+    err(L.moe_grouped_gemm(*args(a=ctypes.c_void_p(0x10008))), -6)
+    err(L.moe_grouped_swiglu(FAKE, FAKE, None, FAKE, 4, 64, 128, 256, None, 0, FAKE, ws, 4096,
+                             None), -1)
+    assert L.moe_grouped_gemm_workspace_bytes(64) == 512
+    assert L.moe_grouped_gemm_workspace_bytes(0) == 256
+    assert L.moe_grouped_gemm_workspace_bytes(-1) == 0
+
+
 def test_python_layer_refuses_cpu_tensors():
     x = torch.zeros(4, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="no CPU path"):

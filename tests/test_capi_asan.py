@@ -18,8 +18,8 @@ def test_capi_validation_under_asan():
     tmp = tempfile.mkdtemp(prefix="moe_asan_")
     try:
         exe = os.path.join(tmp, "capi_validation")
-        srcs = [os.path.join(CSRC, f) for f in ("router_gemm.hip", "topk.hip", "dispatch.hip",
-                                                  "permute.hip", "combine.hip", "moe_capi.cpp")]
+        from moe_route.build import SOURCES
+        srcs = [os.path.join(CSRC, f) for f in SOURCES]
         cmd = [HIPCC, "-O1", "-g", "-std=c++17", "--offload-arch=gfx950",
                "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -17,6 +17,10 @@ function is pinned here by something other than its own formula:
 | fp8_quant_rows        | hand e4m3fn decoder + brute-force nearest-even over all 256 codes |
 | combine               | identity experts return x (C1 closed form); float64 loop          |
 | router_logits         | float64 matmul with the fp32 summation error bound               |
+| group_bounds          | brute-force row -> group lookup (searchsorted); clamping cases    |
+| grouped_gemm          | float64 per-row loop over each row's own group; identity weights |
+|                       | return a; identity shortcut reads ident_a                         |
+| grouped_swiglu        | float64 math.exp closed form x / (1 + e^-x) * u                   |
 """
 import itertools
 import math
@@ -293,3 +297,73 @@ def test_wsplit_hi_lo_reconstructs_fp32():
     rec = hi.double() + lo.double()
     # hi+lo carries 16 significant bits: relative error <= 2^-16
     assert ((rec - w.double()).abs() <= w.double().abs() * 2.0 ** -16).all()
+
+
+# ---------------------------------------------------------------- grouped GEMM
+def _ragged_offsets(sizes):
+    return np.cumsum(np.asarray(sizes, dtype=np.int64)).astype(np.int32)
+
+
+def test_group_bounds_brute_force_and_clamps():
+    sizes = [3, 0, 5, 0, 0, 1, 7]
+    offs = _ragged_offsets(sizes)
+    M = int(offs[-1])
+    b = O.group_bounds(offs, M)
+    # row -> group by a lookup independent of the scan: first group whose end exceeds the row
+    for r in range(M):
+        g = int(np.searchsorted(offs, r, side="right"))
+        assert b[g][0] <= r < b[g][1]
+        assert sum(lo <= r < hi for lo, hi in b) == 1
+    assert [hi - lo for lo, hi in b] == sizes
+    # out-of-range ends are clamped into [0, M]; a group is never negative-sized;
+    # each group starts at the previous raw end (clamped), as the device plan reads it
+    assert O.group_bounds(np.array([5, 2, 40], np.int32), 10) == [(0, 5), (5, 5), (2, 10)]
+    assert O.group_bounds(np.array([-3, 4], np.int32), 4) == [(0, 0), (0, 4)]
+
+
+def test_grouped_gemm_vs_float64_per_row_loop():
+    g = torch.Generator().manual_seed(5)
+    sizes = [4, 0, 9, 1, 0, 6]
+    offs = _ragged_offsets(sizes)
+    M, N, K, G = int(offs[-1]), 7, 12, len(sizes)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = torch.randn(G, N, K, generator=g).to(torch.bfloat16)
+    got = O.grouped_gemm(a, w, offs).double().numpy()
+    A, W = a.double().numpy(), w.double().numpy()
+    for r in range(M):
+        gi = int(np.searchsorted(offs, r, side="right"))
+        for n in range(N):
+            ref = math.fsum(A[r, kk] * W[gi, n, kk] for kk in range(K))
+            bound = K * 2.0 ** -24 * sum(abs(A[r, kk] * W[gi, n, kk]) for kk in range(K))
+            assert abs(got[r, n] - ref) <= bound + 1e-30
+
+
+def test_grouped_gemm_identity_weights_and_shortcut():
+    g = torch.Generator().manual_seed(6)
+    sizes = [3, 5, 2]
+    offs = _ragged_offsets(sizes)
+    M, K, G = int(offs[-1]), 8, 3
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    eye = torch.eye(K).repeat(G, 1, 1).to(torch.bfloat16)
+    assert torch.equal(O.grouped_gemm(a, eye, offs), a.float())
+    # identity shortcut: the 5-row group reads ident_a instead of a
+    ident = torch.randn(5, K, generator=g).to(torch.bfloat16)
+    got = O.grouped_gemm(a, eye, offs, ident_a=ident, ident_m=5)
+    assert torch.equal(got[3:8], ident.float())
+    assert torch.equal(got[:3], a[:3].float()) and torch.equal(got[8:], a[8:].float())
+
+
+def test_grouped_swiglu_closed_form():
+    g = torch.Generator().manual_seed(7)
+    sizes = [2, 3]
+    offs = _ragged_offsets(sizes)
+    M, N, K = 5, 4, 8
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    eye = torch.eye(N, K).repeat(2, 1, 1).to(torch.bfloat16)        # picks the first N columns
+    two = (2 * torch.eye(N, K)).repeat(2, 1, 1).to(torch.bfloat16)
+    h = O.grouped_swiglu(a, eye, two, offs).double().numpy()
+    A = a.double().numpy()
+    for r in range(M):
+        for n in range(N):
+            x = A[r, n]
+            assert abs(h[r, n] - x / (1.0 + math.exp(-x)) * 2 * x) <= 1e-6 * (1 + abs(h[r, n]))
