@@ -12,6 +12,14 @@ per-stage times, the end-to-end HBM fraction, and the CPU oracle's rate on a
 bounded sample of the same workload (rank 0, N=1).
 
     python bench.py [--steps K] [--warmup W] [--config C4|C5|C2|C3] [--no-cpu]
+    python bench.py --layer [T ...]   # the drop-in run() at the reference's workloads
+
+--layer times the reference entry point run() (route, dispatch, SwiGLU
+experts and shared expert on the grouped GEMM, combine) at the reference's
+own workload shapes (NE=64, H=8192, Ni=3584, SNi=7168, top-8; T from its
+9-workload mix, kernel.cu:133-136) and prints ONE JSON line with per-T
+latency and the mix-weighted sum the reference quotes (35.92 ms on B200,
+kernel.cu:146-151).
 """
 import argparse
 import json
@@ -95,6 +103,56 @@ def cpu_baseline(c, sample_T):
                       "median of 3 = %.3f s" % (sample_T, c.name, sample_T, c.H, c.E, c.k, med)}
 
 
+LAYER_MIX = {1571: 1, 2048: 1, 4096: 3, 4904: 1, 8192: 3}  # kernel.cu:133-136
+
+
+def layer_bench(Ts, steps, warmup):
+    """run() latency per T (HIP events around each call, median of `steps`)."""
+    dev = torch.device("cuda:0")
+    H, E, Ni, SNi = 8192, 64, 3584, 7168
+    g = torch.Generator(device=dev).manual_seed(0)
+    r = lambda *sh: torch.randn(*sh, generator=g, device=dev)
+    gw = r(E, H) / H ** 0.5
+    bias = r(E)
+    eg = (r(E, Ni, H) / H ** 0.5).to(torch.bfloat16)
+    eu = (r(E, Ni, H) / H ** 0.5).to(torch.bfloat16)
+    ed = (r(E, H, Ni) / Ni ** 0.5).to(torch.bfloat16)
+    sg = (r(SNi, H) / H ** 0.5).to(torch.bfloat16)
+    su = (r(SNi, H) / H ** 0.5).to(torch.bfloat16)
+    sd = (r(H, SNi) / SNi ** 0.5).to(torch.bfloat16)
+    ms = {}
+    for T in Ts:
+        hs = r(1, T, H).to(torch.bfloat16)
+        args = (hs, gw, bias, eg, eu, ed, sg, su, sd, 1e-6)
+        for _ in range(warmup):
+            M.run(*args)
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(steps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            M.run(*args)
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        ms[T] = statistics.median(ts)
+        print("layer T=%d: %.3f ms" % (T, ms[T]), file=sys.stderr, flush=True)
+    line = {
+        "metric": "reference run() layer latency (route+dispatch+SwiGLU experts+shared+combine)",
+        "value": round(sum(LAYER_MIX.get(T, 1) * ms[T] for T in Ts), 4), "unit": "ms",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded randn, the reference harness's distributions)",
+        "config": {"workload": "kernel.cu run(): NE=64 H=8192 Ni=3584 SNi=7168 top-8; value = "
+                               "sum over T of mix weight x latency",
+                   "mix": {str(T): LAYER_MIX.get(T, 1) for T in Ts}},
+        "per_T_ms": {str(T): round(v, 4) for T, v in ms.items()},
+        "reference_b200_mix_sum_ms": 35.92,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,11 +164,17 @@ def main():
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one plain 1 GiB device copy (untimed), the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
+    ap.add_argument("--layer", nargs="*", type=int, default=None,
+                    help="time run() at the reference's workload T values (default: its mix)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this path runs on one GPU only (no sharding, no collectives); "
               "--gpus %d is not supported" % args.gpus, file=sys.stderr)
         sys.exit(2)
+
+    if args.layer is not None:
+        layer_bench(args.layer or sorted(LAYER_MIX), max(args.steps // 2, 5), 2)
+        return
 
     c = CONFIGS[args.config]
     dev = torch.device("cuda:0")

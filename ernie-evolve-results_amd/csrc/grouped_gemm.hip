@@ -36,7 +36,7 @@
 
 namespace moe {
 
-constexpr int kGgBM = 256, kGgBN = 256, kGgBK = 64;
+constexpr int kGgBM = 256, kGgBN = 256;
 
 // One workgroup of 1024 threads: inclusive scan of per-group tile counts.
 __global__ __launch_bounds__(1024) void gg_plan_kernel(const int* __restrict__ offs, int G, int M,
@@ -86,16 +86,19 @@ __global__ __launch_bounds__(1024) void gg_plan_kernel(const int* __restrict__ o
 // silu(g) * u in fp32
 __device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
-template <bool SWIGLU>
+template <bool SWIGLU, int BK, int NS>
 __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
     const __bf16* __restrict__ a, const __bf16* __restrict__ ident_a, int ident_m,
     const __bf16* __restrict__ w0, const __bf16* __restrict__ w1,
     const int* __restrict__ offs, const int* __restrict__ tile_start, int G, int M, int N, int K,
     int n_tiles, unsigned short* __restrict__ out) {
-  constexpr int BM = kGgBM, BN = kGgBN, BK = kGgBK, NS = 2, CH = 8, ROWB = 128, RPI = 8;
+  // BK = 64: 128-byte LDS rows (8 chunks of 16 B); BK = 32: 64-byte rows (4 chunks).
+  // A DMA wave instruction moves 1 KB = RPI rows.
+  constexpr int BM = kGgBM, BN = kGgBN, ROWB = BK * 2, CH = ROWB / 16, RPI = 1024 / ROWB;
   constexpr int STAGE_B = (BM + BN) * ROWB;
   constexpr int A_INST = BM / RPI, B_INST = BN / RPI, NW = 16, PER_WAVE = (A_INST + B_INST) / NW;
   constexpr int WM = 4, WN = 4, WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
+  static_assert(BK == 32 || BK == 64, "K step of one or two MFMA depths");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B];
 
   // XCD-aware order: gridDim.x is a multiple of 8, hardware block b runs on
@@ -119,7 +122,9 @@ __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  auto swz = [](int r) { return (r >> 1) & (CH - 1); };
+  // logical chunk c of LDS row r sits at c ^ swz(r): the 16 rows of one
+  // fragment read fall on distinct bank groups
+  auto swz = [](int r) { return CH == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
   const long long wbase = (long long)g * N * K;
 
   const __bf16* src[PER_WAVE];
@@ -163,14 +168,20 @@ __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / BK;
-  issue(0, 0);
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < KT) issue(st, st);
   const int fr = lane & 15, fc = lane >> 4;
   for (int kt = 0; kt < KT; ++kt) {
-    // stage kt landed (this wave's DMA), then the barrier publishes every
-    // wave's DMA and retires all reads of the buffer reloaded next
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kt + 1 < KT) issue(kt + 1, (kt + 1) & 1);
-    const char* sb = lds + (kt & 1) * STAGE_B;
+    // this wave's stage kt landed once at most the NS-2 later stages are
+    // outstanding; the barrier then publishes every wave's DMA and retires
+    // all reads of the buffer reloaded next
+    if (kt + NS - 2 < KT)
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (kt + NS - 1 < KT) issue(kt + NS - 1, (kt + NS - 1) % NS);
+    const char* sb = lds + (kt % NS) * STAGE_B;
 #pragma unroll
     for (int kk = 0; kk < BK / 32; ++kk) {
       bf16x8 av[FM], bv[FN];
@@ -222,7 +233,29 @@ int grouped_gemm_n_tiles(int N, bool swiglu) {
   return (N + per - 1) / per;
 }
 
+template <int BK, int NS>
+static hipError_t launch_gg(const void* a, const void* ident_a, int ident_m, const void* w0,
+                            const void* w1, const int32_t* offs, int G, int M, int N, int K,
+                            bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
+  const int n_tiles = grouped_gemm_n_tiles(N, swiglu);
+  const long long m_bound = ((long long)M + kGgBM - 1) / kGgBM + G;
+  long long blocks = m_bound * n_tiles;
+  blocks = (blocks + 7) / 8 * 8;
+  const dim3 grid((unsigned)blocks), blk(1024);
+  if (swiglu)
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, BK, NS>), grid, blk, 0, s, (const __bf16*)a,
+                       (const __bf16*)ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1,
+                       offs, tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, BK, NS>), grid, blk, 0, s, (const __bf16*)a,
+                       (const __bf16*)ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0,
+                       offs, tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
+  return hipGetLastError();
+}
+
 // tile_start: [G+1] ints of workspace.  offs: inclusive group ends (device).
+// BK = 64 with a 2-stage ring measured fastest on MI355X at the reference's
+// expert shapes (BK = 32 with 3 or 4 stages: 8-13% slower, same results).
 hipError_t launch_grouped_gemm(const void* a, const void* ident_a, int ident_m, const void* w0,
                                const void* w1, const int32_t* offs, int G, int M, int N, int K,
                                bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
@@ -230,20 +263,8 @@ hipError_t launch_grouped_gemm(const void* a, const void* ident_a, int ident_m, 
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (M == 0 || N == 0 || G == 0) return hipSuccess;
-  const int n_tiles = grouped_gemm_n_tiles(N, swiglu);
-  const long long m_bound = ((long long)M + kGgBM - 1) / kGgBM + G;
-  long long blocks = m_bound * n_tiles;
-  blocks = (blocks + 7) / 8 * 8;
-  const dim3 grid((unsigned)blocks), blk(1024);
-  if (swiglu)
-    hipLaunchKernelGGL(grouped_gemm_kernel<true>, grid, blk, 0, s, (const __bf16*)a,
-                       (const __bf16*)ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1,
-                       offs, tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
-  else
-    hipLaunchKernelGGL(grouped_gemm_kernel<false>, grid, blk, 0, s, (const __bf16*)a,
-                       (const __bf16*)ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0,
-                       offs, tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
-  return hipGetLastError();
+  return launch_gg<64, 2>(a, ident_a, ident_m, w0, w1, offs, G, M, N, K, swiglu, out,
+                          tile_start, s);
 }
 
 }  // namespace moe
