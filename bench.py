@@ -106,7 +106,7 @@ def cpu_baseline(c, sample_T):
 LAYER_MIX = {1571: 1, 2048: 1, 4096: 3, 4904: 1, 8192: 3}  # kernel.cu:133-136
 
 
-def layer_bench(Ts, steps, warmup):
+def layer_bench(Ts, steps, warmup, dispatch="bf16"):
     """run() latency per T (HIP events around each call, median of `steps`)."""
     dev = torch.device("cuda:0")
     H, E, Ni, SNi = 8192, 64, 3584, 7168
@@ -124,15 +124,16 @@ def layer_bench(Ts, steps, warmup):
     for T in Ts:
         hs = r(1, T, H).to(torch.bfloat16)
         args = (hs, gw, bias, eg, eu, ed, sg, su, sd, 1e-6)
+        run = lambda: M.run(*args, dispatch=dispatch)
         for _ in range(warmup):
-            M.run(*args)
+            run()
         torch.cuda.synchronize()
         ts = []
         for _ in range(steps):
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record()
-            M.run(*args)
+            run()
             b.record()
             b.synchronize()
             ts.append(a.elapsed_time(b))
@@ -146,6 +147,7 @@ def layer_bench(Ts, steps, warmup):
         "data": "synthetic (seeded randn, the reference harness's distributions)",
         "config": {"workload": "kernel.cu run(): NE=64 H=8192 Ni=3584 SNi=7168 top-8; value = "
                                "sum over T of mix weight x latency",
+                   "dispatch": dispatch,
                    "mix": {str(T): LAYER_MIX.get(T, 1) for T in Ts}},
         "per_T_ms": {str(T): round(v, 4) for T, v in ms.items()},
         "reference_b200_mix_sum_ms": 35.92,
@@ -166,6 +168,8 @@ def main():
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
     ap.add_argument("--layer", nargs="*", type=int, default=None,
                     help="time run() at the reference's workload T values (default: its mix)")
+    ap.add_argument("--layer-fp8", action="store_true",
+                    help="with --layer: run(..., dispatch='fp8')")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this path runs on one GPU only (no sharding, no collectives); "
@@ -173,7 +177,8 @@ def main():
         sys.exit(2)
 
     if args.layer is not None:
-        layer_bench(args.layer or sorted(LAYER_MIX), max(args.steps // 2, 5), 2)
+        layer_bench(args.layer or sorted(LAYER_MIX), max(args.steps // 2, 5), 2,
+                    "fp8" if args.layer_fp8 else "bf16")
         return
 
     c = CONFIGS[args.config]

@@ -86,20 +86,50 @@ __global__ __launch_bounds__(1024) void gg_plan_kernel(const int* __restrict__ o
 // silu(g) * u in fp32
 __device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + __expf(-g)) * u; }
 
-template <bool SWIGLU, int BK, int NS>
+// 16 e4m3fn bytes -> 16 bf16(q * s): exact fp8 -> fp32 conversion, one fp32
+// multiply, and the gfx950 fp32 -> bf16 conversion (round to nearest even).
+__device__ __forceinline__ void dequant16(u32x4 raw, float s, bf16x8& lo8, bf16x8& hi8) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw[h], false);
+    const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)raw[h], true);
+    bf16x8& d = h < 2 ? lo8 : hi8;
+    const int o = (h & 1) * 4;
+    d[o + 0] = (__bf16)(a[0] * s);
+    d[o + 1] = (__bf16)(a[1] * s);
+    d[o + 2] = (__bf16)(b[0] * s);
+    d[o + 3] = (__bf16)(b[1] * s);
+  }
+}
+
+template <bool SWIGLU, bool AFP8, int BK, int NS>
 __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
-    const __bf16* __restrict__ a, const __bf16* __restrict__ ident_a, int ident_m,
-    const __bf16* __restrict__ w0, const __bf16* __restrict__ w1,
+    const void* __restrict__ a_, const float* __restrict__ a_scales, const void* __restrict__ ident_,
+    int ident_m, const __bf16* __restrict__ w0, const __bf16* __restrict__ w1,
     const int* __restrict__ offs, const int* __restrict__ tile_start, int G, int M, int N, int K,
     int n_tiles, unsigned short* __restrict__ out) {
-  // BK = 64: 128-byte LDS rows (8 chunks of 16 B); BK = 32: 64-byte rows (4 chunks).
-  // A DMA wave instruction moves 1 KB = RPI rows.
-  constexpr int BM = kGgBM, BN = kGgBN, ROWB = BK * 2, CH = ROWB / 16, RPI = 1024 / ROWB;
-  constexpr int STAGE_B = (BM + BN) * ROWB;
-  constexpr int A_INST = BM / RPI, B_INST = BN / RPI, NW = 16, PER_WAVE = (A_INST + B_INST) / NW;
+  // LDS rows: B (weights, bf16) BK*2 bytes; A BK*2 bytes (bf16) or BK bytes (fp8).
+  // A DMA wave instruction moves 1 KB = 1024 / row-bytes rows.
+  constexpr int BM = kGgBM, BN = kGgBN;
+  constexpr int ROWB = BK * 2, CH = ROWB / 16, RPI = 1024 / ROWB;
+  constexpr int AROWB = AFP8 ? BK : BK * 2, ACH = AROWB / 16, ARPI = 1024 / AROWB;
+  constexpr int A_BYTES = BM * AROWB, STAGE_B = A_BYTES + BN * ROWB;
+  // fp8 A: the DMA stages hold the e4m3fn bytes; each K step they are
+  // dequantised once, cooperatively, into one bf16 tile (BM x BK) that the
+  // fragment reads use.
+  constexpr int DQ_BYTES = AFP8 ? BM * BK * 2 : 0;
+  constexpr int A_INST = BM / ARPI, B_INST = BN / RPI, NW = 16, PER_WAVE = (A_INST + B_INST) / NW;
   constexpr int WM = 4, WN = 4, WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
   static_assert(BK == 32 || BK == 64, "K step of one or two MFMA depths");
-  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B];
+  static_assert((A_INST + B_INST) % NW == 0, "every wave issues the same number of loads");
+  static_assert(!AFP8 || BK == 64, "fp8 A: one 128-wide scale block spans two K steps");
+  static_assert(!AFP8 || BM * ACH == 1024, "fp8 A: one 16-byte chunk per thread per K step");
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B + DQ_BYTES];
+  char* const dq = lds + NS * STAGE_B;
+  const char* a = (const char*)a_;
+  const char* ident_a = (const char*)ident_;
+  constexpr int AEL = AFP8 ? 1 : 2;  // bytes per A element
 
   // XCD-aware order: gridDim.x is a multiple of 8, hardware block b runs on
   // XCD b % 8; logical tiles [x*nb/8, (x+1)*nb/8) all run on XCD x.
@@ -122,23 +152,26 @@ __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
-  // logical chunk c of LDS row r sits at c ^ swz(r): the 16 rows of one
-  // fragment read fall on distinct bank groups
-  auto swz = [](int r) { return CH == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
+  // logical 16-byte chunk c of an LDS row r sits at c ^ swz(r): the 16 rows
+  // of one fragment read fall on distinct bank groups
+  auto swz = [](int r, int ch) { return ch == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
   const long long wbase = (long long)g * N * K;
 
-  const __bf16* src[PER_WAVE];
+  // DMA sources (bytes) and the byte advance per K step of each instruction
+  const char* src[PER_WAVE];
+  int kstep[PER_WAVE];
 #pragma unroll
   for (int q = 0; q < PER_WAVE; ++q) {
     const int gi = wave * PER_WAVE + q;
-    const int p = lane % CH;
     if (gi < A_INST) {
-      const int r = gi * RPI + lane / CH;
+      const int r = gi * ARPI + lane / ACH, p = lane % ACH;
       const int row = min(r0 + r, rlast);  // rows past the group are loaded, never stored
-      const __bf16* arow = ident ? ident_a + (long long)(row - gs) * K : a + (long long)row * K;
-      src[q] = arow + (p ^ swz(r)) * 8;
+      const char* arow = ident ? ident_a + (long long)(row - gs) * K * AEL
+                               : a + (long long)row * K * AEL;
+      src[q] = arow + (p ^ swz(r, ACH)) * 16;
+      kstep[q] = BK * AEL;
     } else {
-      const int r = (gi - A_INST) * RPI + lane / CH;
+      const int r = (gi - A_INST) * RPI + lane / CH, p = lane % CH;
       int wrow;
       const __bf16* wsrc = w0;
       if (SWIGLU) {
@@ -149,7 +182,8 @@ __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
         wrow = nt * BN + r;
       }
       wrow = min(wrow, N - 1);
-      src[q] = wsrc + wbase + (long long)wrow * K + (p ^ swz(r)) * 8;
+      src[q] = (const char*)(wsrc + wbase + (long long)wrow * K) + (p ^ swz(r, CH)) * 16;
+      kstep[q] = BK * 2;
     }
   }
   auto issue = [&](int kt, int st) {
@@ -157,9 +191,23 @@ __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
     for (int q = 0; q < PER_WAVE; ++q) {
       auto* dst = (__attribute__((address_space(3))) void*)(lds + st * STAGE_B +
                                                             (wave * PER_WAVE + q) * 1024);
-      __builtin_amdgcn_global_load_lds((const void*)(src[q] + kt * BK), dst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(src[q] + (long long)kt * kstep[q]), dst, 16,
+                                       0, 0);
     }
   };
+
+  // fp8: thread t dequantises 16 bytes (chunk t % 4) of tile row t / 4 every
+  // K step; it keeps that row's scale for the current 128-wide K block and
+  // the next block's, loaded one block ahead.
+  const int fr = lane & 15, fc = lane >> 4;
+  const int nsb = K / 128;
+  const int dq_r = threadIdx.x >> 2, dq_c = threadIdx.x & 3;
+  const float* dq_srow = a_scales + (long long)min(r0 + dq_r, rlast) * nsb;
+  float sc = 0.0f, scn = 0.0f;
+  if (AFP8) {
+    sc = dq_srow[0];
+    scn = nsb > 1 ? dq_srow[1] : 0.0f;
+  }
 
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -171,7 +219,6 @@ __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
     if (st < KT) issue(st, st);
-  const int fr = lane & 15, fc = lane >> 4;
   for (int kt = 0; kt < KT; ++kt) {
     // this wave's stage kt landed once at most the NS-2 later stages are
     // outstanding; the barrier then publishes every wave's DMA and retires
@@ -182,18 +229,36 @@ __global__ __launch_bounds__(1024) void grouped_gemm_kernel(
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     if (kt + NS - 1 < KT) issue(kt + NS - 1, (kt + NS - 1) % NS);
     const char* sb = lds + (kt % NS) * STAGE_B;
+    if (AFP8) {
+      if (kt > 0 && (kt & 1) == 0) {  // a new 128-wide scale block starts
+        sc = scn;
+        scn = (kt >> 1) + 1 < nsb ? dq_srow[(kt >> 1) + 1] : 0.0f;
+      }
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(
+          sb + dq_r * AROWB + ((dq_c ^ swz(dq_r, ACH)) * 16));
+      bf16x8 lo8, hi8;
+      dequant16(raw, sc, lo8, hi8);
+      *reinterpret_cast<bf16x8*>(dq + dq_r * ROWB + (((2 * dq_c) ^ swz(dq_r, CH)) * 16)) = lo8;
+      *reinterpret_cast<bf16x8*>(dq + dq_r * ROWB + (((2 * dq_c + 1) ^ swz(dq_r, CH)) * 16)) = hi8;
+      // the bf16 tile is complete for every wave (its previous contents were
+      // retired by the barrier at the top of this step)
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+    }
 #pragma unroll
     for (int kk = 0; kk < BK / 32; ++kk) {
-      bf16x8 av[FM], bv[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int r = wm * WTM + i * 16 + fr, c = kk * 4 + fc;
-        av[i] = *reinterpret_cast<const bf16x8*>(sb + r * ROWB + ((c ^ swz(r)) * 16));
-      }
+      bf16x8 bv[FN];
 #pragma unroll
       for (int j = 0; j < FN; ++j) {
         const int r = wn * WTN + j * 16 + fr, c = kk * 4 + fc;
-        bv[j] = *reinterpret_cast<const bf16x8*>(sb + BM * ROWB + r * ROWB + ((c ^ swz(r)) * 16));
+        bv[j] = *reinterpret_cast<const bf16x8*>(sb + A_BYTES + r * ROWB + ((c ^ swz(r, CH)) * 16));
+      }
+      bf16x8 av[FM];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = wm * WTM + i * 16 + fr, c = kk * 4 + fc;
+        av[i] = AFP8 ? *reinterpret_cast<const bf16x8*>(dq + r * ROWB + ((c ^ swz(r, CH)) * 16))
+                     : *reinterpret_cast<const bf16x8*>(sb + r * AROWB + ((c ^ swz(r, ACH)) * 16));
       }
 #pragma unroll
       for (int i = 0; i < FM; ++i)
@@ -233,37 +298,43 @@ int grouped_gemm_n_tiles(int N, bool swiglu) {
   return (N + per - 1) / per;
 }
 
-template <int BK, int NS>
-static hipError_t launch_gg(const void* a, const void* ident_a, int ident_m, const void* w0,
-                            const void* w1, const int32_t* offs, int G, int M, int N, int K,
-                            bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
+template <bool AFP8>
+static hipError_t launch_gg(const void* a, const float* a_scales, const void* ident_a, int ident_m,
+                            const void* w0, const void* w1, const int32_t* offs, int G, int M, int N,
+                            int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
   const int n_tiles = grouped_gemm_n_tiles(N, swiglu);
   const long long m_bound = ((long long)M + kGgBM - 1) / kGgBM + G;
   long long blocks = m_bound * n_tiles;
   blocks = (blocks + 7) / 8 * 8;
   const dim3 grid((unsigned)blocks), blk(1024);
   if (swiglu)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, BK, NS>), grid, blk, 0, s, (const __bf16*)a,
-                       (const __bf16*)ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1,
-                       offs, tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, 64, 2>), grid, blk, 0, s, a, a_scales,
+                       ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1, offs, tile_start, G,
+                       M, N, K, n_tiles, (unsigned short*)out);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, BK, NS>), grid, blk, 0, s, (const __bf16*)a,
-                       (const __bf16*)ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0,
-                       offs, tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, 64, 2>), grid, blk, 0, s, a, a_scales,
+                       ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0, offs, tile_start, G,
+                       M, N, K, n_tiles, (unsigned short*)out);
   return hipGetLastError();
 }
 
 // tile_start: [G+1] ints of workspace.  offs: inclusive group ends (device).
-// BK = 64 with a 2-stage ring measured fastest on MI355X at the reference's
-// expert shapes (BK = 32 with 3 or 4 stages: 8-13% slower, same results).
-hipError_t launch_grouped_gemm(const void* a, const void* ident_a, int ident_m, const void* w0,
-                               const void* w1, const int32_t* offs, int G, int M, int N, int K,
-                               bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
+// a_scales == NULL: a is bf16.  Else a is e4m3fn bytes with one fp32 scale per
+// row and 128-wide K block ([M, K/128]).  BK = 64 with a 2-stage ring
+// measured fastest on MI355X at the reference's expert shapes (BK = 32 with
+// 3 or 4 stages: 8-13% slower, same results).
+hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const void* ident_a,
+                               int ident_m, const void* w0, const void* w1, const int32_t* offs,
+                               int G, int M, int N, int K, bool swiglu, void* out,
+                               int32_t* tile_start, hipStream_t s) {
   hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, tile_start);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (M == 0 || N == 0 || G == 0) return hipSuccess;
-  return launch_gg<64, 2>(a, ident_a, ident_m, w0, w1, offs, G, M, N, K, swiglu, out,
+  if (a_scales)
+    return launch_gg<true>(a, a_scales, ident_a, ident_m, w0, w1, offs, G, M, N, K, swiglu, out,
+                           tile_start, s);
+  return launch_gg<false>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M, N, K, swiglu, out,
                           tile_start, s);
 }
 

@@ -271,12 +271,20 @@ size_t moe_grouped_gemm_workspace_bytes(int G) {
   return round256((size_t)(G + 1) * 4);
 }
 
-static int grouped_common(const void* a, const void* w0, const void* w1, const int32_t* offs,
-                          int G, int M, int N, int K, const void* ident_a, int ident_m,
-                          void* out, void* ws, size_t ws_bytes, void* stream, bool swiglu) {
+static int grouped_common(const void* a, const float* a_scales, const void* w0, const void* w1,
+                          const int32_t* offs, int G, int M, int N, int K, const void* ident_a,
+                          int ident_m, void* out, void* ws, size_t ws_bytes, void* stream,
+                          bool swiglu, bool fp8) {
   if (G < 1 || G > 65536) return fail(MOE_ERR_INVALID_ARG, "G=%d not in [1, 65536]", G);
   if (M < 0 || N < 1 || K < 1) return fail(MOE_ERR_INVALID_ARG, "M=%d, N=%d, K=%d", M, N, K);
   if (K % 64 != 0) return fail(MOE_ERR_UNSUPPORTED, "K=%d is not a multiple of 64", K);
+  if (fp8) {
+    if (K % 128 != 0)
+      return fail(MOE_ERR_UNSUPPORTED, "fp8 A needs K %% 128 == 0 (one scale per 128), K=%d", K);
+    if (M > 0 && !a_scales) return fail(MOE_ERR_NULL_POINTER, "fp8 A needs a_scales");
+    if (a_scales && ((uintptr_t)a_scales & 3u))
+      return fail(MOE_ERR_ALIGNMENT, "a_scales not 4-byte aligned");
+  }
   if (ident_m < 0) return fail(MOE_ERR_INVALID_ARG, "ident_m=%d < 0", ident_m);
   if (!offs || !ws) return fail(MOE_ERR_NULL_POINTER, "offs and ws are required");
   if (M > 0 && (!a || !w0 || !w1 || !out))
@@ -294,23 +302,38 @@ static int grouped_common(const void* a, const void* w0, const void* w1, const i
   const long long blocks = (((long long)M + 255) / 256 + G) *
                            moe::grouped_gemm_n_tiles(N, swiglu);
   if (blocks >= (1ll << 31)) return fail(MOE_ERR_UNSUPPORTED, "too many tiles (%lld)", blocks);
-  return launched(moe::launch_grouped_gemm(a, ident_a, ident_m, w0, w1, offs, G, M, N, K, swiglu,
-                                           out, (int32_t*)ws, (hipStream_t)stream),
+  return launched(moe::launch_grouped_gemm(a, fp8 ? a_scales : nullptr, ident_a, ident_m, w0, w1,
+                                           offs, G, M, N, K, swiglu, out, (int32_t*)ws,
+                                           (hipStream_t)stream),
                   swiglu ? "grouped_swiglu" : "grouped_gemm");
 }
 
 int moe_grouped_gemm(const void* a, const void* w, const int32_t* offs, int G, int M, int N,
                      int K, const void* ident_a, int ident_m, void* out, void* ws,
                      size_t ws_bytes, void* stream) {
-  return grouped_common(a, w, w, offs, G, M, N, K, ident_a, ident_m, out, ws, ws_bytes, stream,
-                        false);
+  return grouped_common(a, nullptr, w, w, offs, G, M, N, K, ident_a, ident_m, out, ws, ws_bytes,
+                        stream, false, false);
 }
 
 int moe_grouped_swiglu(const void* a, const void* wg, const void* wu, const int32_t* offs,
                        int G, int M, int N, int K, const void* ident_a, int ident_m, void* h,
                        void* ws, size_t ws_bytes, void* stream) {
-  return grouped_common(a, wg, wu, offs, G, M, N, K, ident_a, ident_m, h, ws, ws_bytes, stream,
-                        true);
+  return grouped_common(a, nullptr, wg, wu, offs, G, M, N, K, ident_a, ident_m, h, ws, ws_bytes,
+                        stream, true, false);
+}
+
+int moe_grouped_gemm_fp8(const void* a, const float* a_scales, const void* w, const int32_t* offs,
+                         int G, int M, int N, int K, void* out, void* ws, size_t ws_bytes,
+                         void* stream) {
+  return grouped_common(a, a_scales, w, w, offs, G, M, N, K, nullptr, 0, out, ws, ws_bytes,
+                        stream, false, true);
+}
+
+int moe_grouped_swiglu_fp8(const void* a, const float* a_scales, const void* wg, const void* wu,
+                           const int32_t* offs, int G, int M, int N, int K, void* h, void* ws,
+                           size_t ws_bytes, void* stream) {
+  return grouped_common(a, a_scales, wg, wu, offs, G, M, N, K, nullptr, 0, h, ws, ws_bytes,
+                        stream, true, true);
 }
 
 }  // extern "C"

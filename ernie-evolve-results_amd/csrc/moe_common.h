@@ -60,10 +60,12 @@ hipError_t launch_combine(const void* y, int y_dtype, const int32_t* pair_row, c
 
 // Column tiles of the grouped GEMM for N output columns.
 int grouped_gemm_n_tiles(int N, bool swiglu);
-// Expert grouped GEMM (plain or SwiGLU epilogue); tile_start is [G+1] ints of workspace.
-hipError_t launch_grouped_gemm(const void* a, const void* ident_a, int ident_m, const void* w0,
-                               const void* w1, const int32_t* offs, int G, int M, int N, int K,
-                               bool swiglu, void* out, int32_t* tile_start, hipStream_t s);
+// Expert grouped GEMM (plain or SwiGLU epilogue); tile_start is [G+1] ints of
+// workspace; a_scales != NULL selects an e4m3fn A with [M, K/128] fp32 scales.
+hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const void* ident_a,
+                               int ident_m, const void* w0, const void* w1, const int32_t* offs,
+                               int G, int M, int N, int K, bool swiglu, void* out,
+                               int32_t* tile_start, hipStream_t s);
 
 // Experts per lane of the scoring kernel for (E, scoring, n_group).
 int topk_lane_width(int E, int scoring, int n_group);

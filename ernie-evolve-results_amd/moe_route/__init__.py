@@ -31,7 +31,8 @@ ERR_NAMES = {-1: "MOE_ERR_NULL_POINTER", -2: "MOE_ERR_INVALID_ARG", -3: "MOE_ERR
 EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
            "moe_router_gemm", "moe_topk", "moe_route", "moe_offsets",
            "moe_permute_workspace_bytes", "moe_permute", "moe_combine",
-           "moe_grouped_gemm_workspace_bytes", "moe_grouped_gemm", "moe_grouped_swiglu"]
+           "moe_grouped_gemm_workspace_bytes", "moe_grouped_gemm", "moe_grouped_swiglu",
+           "moe_grouped_gemm_fp8", "moe_grouped_swiglu_fp8"]
 
 
 class MoeError(RuntimeError):
@@ -89,6 +90,10 @@ def lib():
         L.moe_grouped_gemm.argtypes = [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _Z, _P]
         L.moe_grouped_swiglu.restype = _I
         L.moe_grouped_swiglu.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _Z, _P]
+        L.moe_grouped_gemm_fp8.restype = _I
+        L.moe_grouped_gemm_fp8.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _Z, _P]
+        L.moe_grouped_swiglu_fp8.restype = _I
+        L.moe_grouped_swiglu_fp8.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _Z, _P]
         _lib = L
     return _lib
 
@@ -240,12 +245,14 @@ def combine(y, pair_row, topk_w, shared=None, out=None):
     return out
 
 
-def _grouped_args(a, offs, ident_a, ident_m):
+def _grouped_args(a, offs, ident_a, ident_m, fp8=False):
     _dev(a, "a")
     _dev(offs, "offs")
     if offs.dtype != torch.int32:
         raise RuntimeError("offs must be int32 inclusive group ends")
-    if a.dtype != torch.bfloat16:
+    if fp8 and a.dtype not in (torch.uint8, torch.float8_e4m3fn):
+        raise RuntimeError("fp8 a must be e4m3fn bytes (uint8 or float8_e4m3fn)")
+    if not fp8 and a.dtype != torch.bfloat16:
         raise RuntimeError("a must be bf16")
     if ident_m and ident_a is None:
         raise RuntimeError("ident_m > 0 needs ident_a")
@@ -286,6 +293,36 @@ def grouped_swiglu(a, wg, wu, offs, ident_a=None, ident_m=0, out=None):
     return out
 
 
+def grouped_gemm_fp8(a, a_scales, w, offs, out=None):
+    """grouped_gemm with an fp8 A operand: a [M,K] e4m3fn bytes and a_scales
+    [M,K/128] fp32 (moe_permute's fp8 output), dequantised in the GEMM's A
+    load as bf16(q * s)."""
+    ws = _grouped_args(a, offs, None, 0, fp8=True)
+    _dev(a_scales, "a_scales")
+    G, N, K = w.shape
+    M = a.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    _check(lib().moe_grouped_gemm_fp8(_ptr(a), _ptr(a_scales), _ptr(w), _ptr(offs), G, M, N, K,
+                                      _ptr(out), _ptr(ws), ws.numel(), _stream(a)))
+    return out
+
+
+def grouped_swiglu_fp8(a, a_scales, wg, wu, offs, out=None):
+    """grouped_swiglu with an fp8 A operand (see grouped_gemm_fp8)."""
+    ws = _grouped_args(a, offs, None, 0, fp8=True)
+    _dev(a_scales, "a_scales")
+    if wg.shape != wu.shape:
+        raise RuntimeError("gate and up weights must have one shape")
+    G, N, K = wg.shape
+    M = a.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    _check(lib().moe_grouped_swiglu_fp8(_ptr(a), _ptr(a_scales), _ptr(wg), _ptr(wu), _ptr(offs),
+                                        G, M, N, K, _ptr(out), _ptr(ws), ws.numel(), _stream(a)))
+    return out
+
+
 def route_dispatch_combine(x, w, bias, y, k, cfg: RouteCfg, fp8=False):
     """The whole path for one batch: route, permute (bf16 or fp8), combine y."""
     logits, ids, wts, counts = route(x, w, bias, k, cfg)
@@ -302,7 +339,8 @@ REF_NE, REF_TOPK = 64, 8  # K:1582-1583
 
 
 def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, expert_up_proj,
-        expert_down_proj, shared_gate_proj, shared_up_proj, shared_down_proj, norm_min):
+        expert_down_proj, shared_gate_proj, shared_up_proj, shared_down_proj, norm_min, *,
+        dispatch="bf16"):
     """Drop-in for the reference's run() (K:4067-4077): returns
     (out [B,S,H] bf16, router_logits [T,64] fp32).
 
@@ -315,7 +353,12 @@ def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, e
                 grouped GEMMs over the device offsets (the reference's CUTLASS
                 grouped GEMMs, moe_gemm.h:66-95);
       shared    the same two kernels with one group of all T rows;
-      combine   out = shared + sum_j w_j y[pair_row]  (K:2365-2428)."""
+      combine   out = shared + sum_j w_j y[pair_row]  (K:2365-2428).
+    dispatch="fp8" (keyword only, not in the reference signature) permutes the
+    routed rows to e4m3fn with per-128 scales and dequantises them inside the
+    expert gate+up GEMM's A load."""
+    if dispatch not in ("bf16", "fp8"):
+        raise RuntimeError("dispatch must be 'bf16' or 'fp8'")
     B, S, H = hidden_states.shape
     T = B * S
     x = hidden_states.reshape(T, H)
@@ -324,9 +367,14 @@ def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, e
     cfg = RouteCfg(SCORING_SOFTMAX_BIAS, True, 1, 1, 1.0, float(norm_min))
     logits, ids, wts, _ = route(x, gate_weight.float().contiguous(),
                                 e_score_correction_bias.float().contiguous(), REF_TOPK, cfg)
-    p = permute(x, ids, E)
+    p = permute(x, ids, E, fp8=dispatch == "fp8")
     ends = p["offsets"][1:]  # inclusive group ends (moe_gemm.h:66-69)
-    h = grouped_swiglu(p["xg"], expert_gate_proj.contiguous(), expert_up_proj.contiguous(), ends)
+    if dispatch == "fp8":
+        h = grouped_swiglu_fp8(p["xg"], p["scales"], expert_gate_proj.contiguous(),
+                               expert_up_proj.contiguous(), ends)
+    else:
+        h = grouped_swiglu(p["xg"], expert_gate_proj.contiguous(), expert_up_proj.contiguous(),
+                           ends)
     y = grouped_gemm(h, expert_down_proj.contiguous(), ends)
     dense = torch.full((1,), T, dtype=torch.int32, device=x.device)
     sh_h = grouped_swiglu(x.contiguous(), shared_gate_proj.contiguous().unsqueeze(0),

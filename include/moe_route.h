@@ -165,6 +165,20 @@ int moe_grouped_swiglu(const void* a, const void* wg, const void* wu, const int3
                        int G, int M, int N, int K, const void* ident_a, int ident_m, void* h,
                        void* ws, size_t ws_bytes, void* stream);
 
+/* fp8 dispatch into the expert GEMMs: the A operand is moe_permute's fp8
+ * output (e4m3fn bytes a [M, K] plus fp32 scales a_scales [M, K/128]) and is
+ * dequantised in the GEMM's A load as bf16(q * s) -- the fp8 row permute
+ * feeding the grouped GEMM without a bf16 copy of the routed rows (the
+ * reference quantises activations for its int8 expert GEMMs the same way,
+ * per row, in xquant: kernel.cu:2542-2596).  Otherwise as moe_grouped_gemm /
+ * moe_grouped_swiglu; needs K % 128 == 0; no identity shortcut. */
+int moe_grouped_gemm_fp8(const void* a, const float* a_scales, const void* w, const int32_t* offs,
+                         int G, int M, int N, int K, void* out, void* ws, size_t ws_bytes,
+                         void* stream);
+int moe_grouped_swiglu_fp8(const void* a, const float* a_scales, const void* wg, const void* wu,
+                           const int32_t* offs, int G, int M, int N, int K, void* h, void* ws,
+                           size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

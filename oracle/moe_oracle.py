@@ -19,6 +19,7 @@ configurations name:
 * dispatch permutation    K:2109-2189 (dispatch_body: inv[s]=pos, tok[pos]=t)
 * gather                  K:2216-2230 (gather_body)
 * combine                 K:2365-2428 (combine_kernel: acc = shared, acc += w*y)
+* fp8 A dequantisation   bf16(q * s) per 1x128 block, the inverse of the fp8 permute
 * expert grouped GEMM     moe_gemm.h:66-95, moe_gemm.cu:616-650 (grouped_mm /
                           grouped_mm_pair over inclusive group ends offs; the
                           SwiGLU h = silu(g) * u of the expert MLP)
@@ -357,6 +358,18 @@ def grouped_gemm(a, w, offs_incl, ident_a=None, ident_m=0):
         if hi > lo:
             out[lo:hi] = _group_a(at, lo, hi, ident_a, ident_m) @ wt[g].float().t()
     return out
+
+
+def dequant_fp8_rows(q, scales):
+    """bf16(float32(q) * s) per 1x128 block: the fp8 row permute's output
+    turned back into the bf16 A operand of the expert GEMM (e4m3fn -> fp32 is
+    exact; one fp32 multiply; round to nearest even).  q [M,K] e4m3fn (or its
+    bytes), scales [M,K/128] fp32."""
+    qt = torch.as_tensor(q)
+    if qt.dtype == torch.uint8:
+        qt = qt.view(torch.float8_e4m3fn)
+    st = torch.as_tensor(scales).float()
+    return (qt.float() * st.repeat_interleave(128, dim=1)).to(torch.bfloat16)
 
 
 def silu(v):

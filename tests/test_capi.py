@@ -135,6 +135,12 @@ def test_grouped_gemm_validation():
     err(L.moe_grouped_gemm(*args(a=ctypes.c_void_p(0x10008))), -6)
     err(L.moe_grouped_swiglu(FAKE, FAKE, None, FAKE, 4, 64, 128, 256, None, 0, FAKE, ws, 4096,
                              None), -1)
+    err(L.moe_grouped_gemm_fp8(FAKE, None, FAKE, FAKE, 4, 64, 128, 256, FAKE, ws, 4096, None), -1,
+        "a_scales")
+    err(L.moe_grouped_gemm_fp8(FAKE, FAKE, FAKE, FAKE, 4, 64, 128, 192, FAKE, ws, 4096, None), -3,
+        "128")
+    err(L.moe_grouped_swiglu_fp8(FAKE, ctypes.c_void_p(0x10002), FAKE, FAKE, FAKE, 4, 64, 128, 256,
+                                 FAKE, ws, 4096, None), -6)
     assert L.moe_grouped_gemm_workspace_bytes(64) == 512
     assert L.moe_grouped_gemm_workspace_bytes(0) == 256
     assert L.moe_grouped_gemm_workspace_bytes(-1) == 0

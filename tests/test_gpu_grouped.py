@@ -168,3 +168,51 @@ def test_grouped_at_reference_expert_shape(cuda):
         ylim = 2.0 ** -8 * yref.abs() + Ni * 2.0 ** -23 * (wd[gi].double().abs() @
                                                             h[r].double().abs())
         assert bool((yerr <= ylim + 1e-30).all()), (r, float((yerr / ylim).max()))
+
+
+# ---------------------------------------------------------------- fp8 A operand
+@pytest.mark.parametrize("sizes,N,K", [
+    ([300, 0, 1, 17, 256], 256, 256),
+    ([9, 70, 0], 200, 128),
+])
+def test_grouped_fp8_equals_bf16_on_dequantised_rows(cuda, sizes, N, K):
+    """The fp8 kernels dequantise A in registers as bf16(q * s) and then run
+    the same MFMA sequence as the bf16 kernels, so they must equal the bf16
+    kernels fed the oracle's dequantised rows bit for bit."""
+    g = torch.Generator().manual_seed(31 + N)
+    G, Mr = len(sizes), int(sum(sizes))
+    x = (torch.randn(Mr, K, generator=g) * 3).to(torch.bfloat16)
+    q, sc = O.fp8_quant_rows(x)
+    a_deq = O.dequant_fp8_rows(q, sc)
+    wg = (torch.randn(G, N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    wu = (torch.randn(G, N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    offs = inclusive(sizes, cuda)
+    qd, sd = q.view(torch.uint8).to(cuda), sc.to(cuda)
+    y8 = M.grouped_gemm_fp8(qd, sd, wg.to(cuda), offs)
+    y16 = M.grouped_gemm(a_deq.to(cuda), wg.to(cuda), offs)
+    h8 = M.grouped_swiglu_fp8(qd, sd, wg.to(cuda), wu.to(cuda), offs)
+    h16 = M.grouped_swiglu(a_deq.to(cuda), wg.to(cuda), wu.to(cuda), offs)
+    torch.cuda.synchronize()
+    assert torch.equal(y8, y16)
+    assert torch.equal(h8, h16)
+    check_plain(y8, a_deq, wg, np.cumsum(sizes))
+
+
+def test_fp8_permute_feeds_grouped_gemm(cuda):
+    """moe_permute(fp8) -> moe_grouped_swiglu_fp8 on real routing equals the
+    bf16 kernel on the oracle's dequantisation of the permuted rows."""
+    T, H, E, k, N = 300, 256, 16, 4, 128
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    wg = (torch.randn(E, N, H, generator=g) / H ** 0.5).to(torch.bfloat16)
+    wu = (torch.randn(E, N, H, generator=g) / H ** 0.5).to(torch.bfloat16)
+    p = M.permute(x.to(cuda), ids.to(cuda), E, fp8=True)
+    ends = p["offsets"][1:]
+    h8 = M.grouped_swiglu_fp8(p["xg"], p["scales"], wg.to(cuda), wu.to(cuda), ends)
+    rt, _ = O.permutation(ids.numpy())
+    q, sc = O.permute_fp8(x, rt)
+    h16 = M.grouped_swiglu(O.dequant_fp8_rows(q, sc).to(cuda), wg.to(cuda), wu.to(cuda), ends)
+    torch.cuda.synchronize()
+    assert torch.equal(p["xg"].cpu().view(torch.uint8), q.view(torch.uint8))
+    assert torch.equal(h8, h16)

@@ -21,6 +21,7 @@ function is pinned here by something other than its own formula:
 | grouped_gemm          | float64 per-row loop over each row's own group; identity weights |
 |                       | return a; identity shortcut reads ident_a                         |
 | grouped_swiglu        | float64 math.exp closed form x / (1 + e^-x) * u                   |
+| dequant_fp8_rows      | hand e4m3fn decoder x scale in numpy fp32, hand bf16 nearest-even |
 """
 import itertools
 import math
@@ -367,3 +368,30 @@ def test_grouped_swiglu_closed_form():
         for n in range(N):
             x = A[r, n]
             assert abs(h[r, n] - x / (1.0 + math.exp(-x)) * 2 * x) <= 1e-6 * (1 + abs(h[r, n]))
+
+
+def _bf16_rne_bits(v32):
+    """fp32 -> bf16 bits by round to nearest even, in integer arithmetic."""
+    u = np.asarray(v32, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_dequant_fp8_rows_hand_decoder():
+    rng = np.random.default_rng(12)
+    x = torch.from_numpy((rng.standard_normal((3, 384)) * 5).astype(f32)).to(torch.bfloat16)
+    q, s = O.fp8_quant_rows(x)
+    got = O.dequant_fp8_rows(q, s).view(torch.int16).numpy().astype(np.uint16)
+    codes = q.view(torch.uint8).numpy()
+    sc = s.numpy()
+    for r in range(3):
+        for i in range(0, 384, 5):
+            prod = np.float32(e4m3fn_decode(int(codes[r, i]))) * np.float32(sc[r, i // 128])
+            assert got[r, i] == _bf16_rne_bits(np.float32(prod)), (r, i)
+    # every one of the 256 codes (NaN codes excluded) at a scale that forces rounding
+    allc = torch.arange(256, dtype=torch.uint8).view(2, 128)
+    keep = [c for c in range(256) if (c & 0x7F) != 0x7F]
+    sc2 = torch.full((2, 1), 1.0 / 3.0)
+    got2 = O.dequant_fp8_rows(allc, sc2).view(torch.int16).numpy().astype(np.uint16).reshape(-1)
+    for c in keep:
+        prod = np.float32(e4m3fn_decode(c)) * np.float32(1.0 / 3.0)
+        assert got2[c] == _bf16_rne_bits(np.float32(prod)), c
