@@ -284,6 +284,9 @@ static int grouped_common(const void* a, const float* a_scales, const void* w0, 
     if (M > 0 && !a_scales) return fail(MOE_ERR_NULL_POINTER, "fp8 A needs a_scales");
     if (a_scales && ((uintptr_t)a_scales & 3u))
       return fail(MOE_ERR_ALIGNMENT, "a_scales not 4-byte aligned");
+    if ((long long)M * (K / 128) >= (1ll << 31))
+      return fail(MOE_ERR_UNSUPPORTED, "a_scales of %lld entries exceeds int32 indexing",
+                  (long long)M * (K / 128));
   }
   if (ident_m < 0) return fail(MOE_ERR_INVALID_ARG, "ident_m=%d < 0", ident_m);
   if (!offs || !ws) return fail(MOE_ERR_NULL_POINTER, "offs and ws are required");

@@ -141,6 +141,8 @@ def test_grouped_gemm_validation():
         "128")
     err(L.moe_grouped_swiglu_fp8(FAKE, ctypes.c_void_p(0x10002), FAKE, FAKE, FAKE, 4, 64, 128, 256,
                                  FAKE, ws, 4096, None), -6)
+    err(L.moe_grouped_gemm_fp8(FAKE, FAKE, FAKE, FAKE, 4, 1 << 24, 128, 1 << 14, FAKE, ws, 4096,
+                               None), -3, "int32")
     assert L.moe_grouped_gemm_workspace_bytes(64) == 512
     assert L.moe_grouped_gemm_workspace_bytes(0) == 256
     assert L.moe_grouped_gemm_workspace_bytes(-1) == 0
