@@ -161,3 +161,26 @@ def test_missing_library_raises(monkeypatch):
     monkeypatch.setattr(M, "LIB_PATH", "/nonexistent/libmoe_route.so")
     with pytest.raises(RuntimeError, match="not built"):
         M.lib()
+
+
+def test_error_string_is_thread_local():
+    """moe_last_error_string() belongs to the calling thread: two threads that
+    fail with different messages each read back their own."""
+    import threading
+    L = M.lib()
+    barrier = threading.Barrier(2)
+    got = {}
+
+    def worker(name, E):
+        rc = L.moe_router_gemm(FAKE, FAKE, 4, 128, E, FAKE, None)
+        barrier.wait()   # both calls have failed before either reads its message
+        got[name] = (rc, L.moe_last_error_string().decode())
+
+    ts = [threading.Thread(target=worker, args=("a", 12)),
+          threading.Thread(target=worker, args=("b", 24))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert got["a"][0] == -3 and "E=12" in got["a"][1]
+    assert got["b"][0] == -3 and "E=24" in got["b"][1]

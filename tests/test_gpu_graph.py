@@ -38,3 +38,31 @@ def test_step_graph_capture_replays(cuda):
         torch.cuda.synchronize()
         for n, v in want.items():
             assert torch.equal(getattr(plan, n), v), (rep, n)
+
+
+def test_two_streams_concurrently(cuda):
+    """Two batches with their own plans (outputs and workspaces) on two
+    default-priority streams at once give exactly the results of running them
+    one after the other: the library keeps no shared device state."""
+    c = CONFIGS["C3"]
+    T = 2048
+    ins = [M.make_inputs(c, T=T, seed=s, device=cuda) for s in (5, 6)]
+    plans = [M.MoePlan(T, c.H, c.E, c.k, c.cfg, cuda) for _ in ins]
+    for p, (x, w, bias, y) in zip(plans, ins):
+        p.step(x, w, bias, y)
+    torch.cuda.synchronize()
+    names = ("logits", "topk_ids", "topk_w", "row_token", "pair_row", "offsets", "xg", "out")
+    want = [{n: getattr(p, n).clone() for n in names} for p in plans]
+    for p in plans:
+        for n in names:
+            getattr(p, n).zero_()
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for _ in range(3):
+        for s, p, (x, w, bias, y) in zip(streams, plans, ins):
+            with torch.cuda.stream(s):
+                p.step(x, w, bias, y)
+    torch.cuda.synchronize()
+    for p, wnt in zip(plans, want):
+        for n, v in wnt.items():
+            assert torch.equal(getattr(p, n), v), n
