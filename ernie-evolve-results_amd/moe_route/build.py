@@ -20,6 +20,10 @@ SOURCES = ["router_gemm.hip", "topk.hip", "dispatch.hip", "permute.hip", "combin
            "grouped_gemm.hip", "moe_capi.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+# A C++ host program that uses the library through its C ABI only (no torch).
+EXAMPLE_SRC = os.path.join(PKG_ROOT, "examples", "moe_step.cpp")
+EXAMPLE_BIN = os.path.join(HERE, "moe_step")
 
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -69,6 +73,13 @@ def build(verbose: bool = False) -> str:
             if l.strip():
                 print(l)
     os.replace(tmp, LIB_PATH)
+    # host-only example against the installed library (rpath: next to the .so)
+    ex = _run(["g++", "-O2", "-std=c++17", EXAMPLE_SRC, "-I", os.path.join(REPO, "include"),
+               "-I", os.path.join(ROCM, "include"), "-D__HIP_PLATFORM_AMD__",
+               "-L", HERE, "-lmoe_route", "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+               "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
+               "-o", EXAMPLE_BIN], verbose)
+    _finish(ex, "examples/moe_step.cpp")
     return LIB_PATH
 
 
