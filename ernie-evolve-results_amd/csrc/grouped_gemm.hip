@@ -17,11 +17,11 @@
 //
 // Tiles: 256 rows x 256 weight rows, 64-wide K steps, staged in LDS by the
 // gfx950 global_load_lds DMA into a 2-stage ring with an XOR-swizzled 16-byte
-// chunk layout, 16 waves with 64 x 64 accumulators of
-// v_mfma_f32_16x16x32_bf16 (the router GEMM's pipeline).  Block ids are
-// remapped so that the n-tiles of one row tile run on one XCD: consecutive
-// logical tiles share the A rows, which then stay in that XCD's L2, while
-// every weight tile is read from HBM once per row tile.
+// chunk layout, v_mfma_f32_16x16x32_bf16 accumulators (bf16 A: 8 waves of
+// 64 x 128 with a software-pipelined K loop; fp8 A: 16 waves of 64 x 64).
+// Block ids are remapped so that each XCD runs a contiguous range of logical
+// tiles, and inside a group the tiles go in 4 x 8 (row x column) super-tiles:
+// the blocks running together on one XCD share A and weight slices in L2.
 //
 // swiglu interleaves the two weights at 16-row granularity inside the B
 // tile (rows 16f..16f+15 come from wg for even f, from wu for odd f), so the
@@ -103,7 +103,17 @@ __device__ __forceinline__ void dequant16(u32x4 raw, float s, bf16x8& lo8, bf16x
   }
 }
 
-template <bool SWIGLU, bool AFP8, int BK, int NS, int WM, int WN>
+// 32-bit LDS address of a __shared__ location, for inline-asm LDS reads.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
+}
+// One 16-byte LDS fragment read issued as an instruction the compiler does not
+// track: the pipelined loop below places its own lgkmcnt waits, which lets a
+// K step's fragment reads stay in flight across the next MFMA group.
+#define MOE_DS_READ_B128(dst, addr, off) \
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(off))
+
+template <bool SWIGLU, bool AFP8, int BK, int NS, int WM, int WN, bool PIPE>
 __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     const void* __restrict__ a_, const float* __restrict__ a_scales, const void* __restrict__ ident_,
     int ident_m, const __bf16* __restrict__ w0, const __bf16* __restrict__ w1,
@@ -127,6 +137,8 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   static_assert(!AFP8 || BK == 64, "fp8 A: one 128-wide scale block spans two K steps");
   static_assert(!AFP8 || (BM * ACH) % NT == 0, "fp8 A: whole 16-byte chunks per thread per K step");
   static_assert(!SWIGLU || FN % 2 == 0, "swiglu: gate/up fragment pairs inside one wave");
+  static_assert(!PIPE || (!AFP8 && BK == 64 && NS == 2 && WM == 4 && WN == 2),
+                "pipelined loop: bf16 A, 2 stages of 64, 8 waves of 64 x 128");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B + DQ_BYTES];
   char* const dq = lds + NS * STAGE_B;
   const char* a = (const char*)a_;
@@ -137,18 +149,32 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   // XCD b % 8; logical tiles [x*nb/8, (x+1)*nb/8) all run on XCD x.
   const unsigned nb = gridDim.x, b = blockIdx.x;
   const unsigned l = (b & 7u) * (nb >> 3) + (b >> 3);
-  const int mt = (int)(l / (unsigned)n_tiles), nt = (int)(l % (unsigned)n_tiles);
-  if (mt >= tile_start[G]) return;
-  // group of this row tile: the last g with tile_start[g] <= mt
+  // Logical tiles are numbered group by group: group g owns
+  // [tile_start[g] * n_tiles, tile_start[g+1] * n_tiles).
+  if (l / (unsigned)n_tiles >= (unsigned)tile_start[G]) return;
+  const int lt = (int)(l / (unsigned)n_tiles);
+  // group of this tile: the last g with tile_start[g] <= lt
   int lo = 0, hi = G - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (tile_start[mid] <= mt) lo = mid; else hi = mid - 1;
+    if (tile_start[mid] <= lt) lo = mid; else hi = mid - 1;
   }
   const int g = lo;
+  // Inside a group, column blocks of kSuperN n-tiles, row tiles across each
+  // block, n fastest: 32 consecutive tiles (one XCD's co-running blocks) are
+  // 4 row tiles x 8 weight tiles, so each A slice and each weight slice of a
+  // K step is fetched from HBM once and then reused from that XCD's L2.
+  constexpr int kSuperN = 8;
+  const int mtg = tile_start[g + 1] - tile_start[g];
+  const int li = (int)l - tile_start[g] * n_tiles;
+  const int nblk = li / (mtg * kSuperN);
+  const int rem = li - nblk * mtg * kSuperN;
+  const int ncols = min(kSuperN, n_tiles - nblk * kSuperN);
+  const int mt_local = rem / ncols;
+  const int nt = nblk * kSuperN + rem % ncols;
   const int gs = g > 0 ? min(max(offs[g - 1], 0), M) : 0;
   const int ge = min(max(offs[g], 0), M);
-  const int r0 = gs + (mt - tile_start[g]) * BM;   // first row of the tile
+  const int r0 = gs + mt_local * BM;               // first row of the tile
   const int rlast = ge - 1;                        // last row of the group
   const bool ident = ident_m > 0 && ge - gs == ident_m;
 
@@ -221,59 +247,129 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int KT = K / BK;
+  if constexpr (PIPE) {
+    // Software-pipelined K loop.  Per K step the wave reads its fragments in
+    // two halves (kk = 0, 1: 4 A + 8 B reads each).  The kk = 1 reads are
+    // issued before the kk = 0 MFMAs, and the next step's kk = 0 reads are
+    // issued right after the barrier, before the kk = 1 MFMAs.  The LDS
+    // latency thus hides behind MFMA work instead of stalling every step.
+    // The MFMA order per accumulator is the same as the plain loop's (K steps
+    // ascending, kk = 0 then 1), so the results are bit-identical to it.
+    const unsigned l0 = lds_addr(lds);
+    unsigned abase[2][2], bbase[2][2];  // [stage][kk]: fragment 0; fragment i / j at +i*2048 / +j*2048
 #pragma unroll
-  for (int st = 0; st < NS - 1; ++st)
-    if (st < KT) issue(st, st);
-  for (int kt = 0; kt < KT; ++kt) {
-    // this wave's stage kt landed once at most the NS-2 later stages are
-    // outstanding; the barrier then publishes every wave's DMA and retires
-    // all reads of the buffer reloaded next
-    if (kt + NS - 2 < KT)
-      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (kt + NS - 1 < KT) issue(kt + NS - 1, (kt + NS - 1) % NS);
-    const char* sb = lds + (kt % NS) * STAGE_B;
-    if (AFP8) {
-      const bool nb = kt > 0 && (kt & 1) == 0;  // a new 128-wide scale block starts
+    for (int st = 0; st < 2; ++st)
 #pragma unroll
-      for (int u = 0; u < DQ_PER; ++u) {
-        if (nb) {
-          sc[u] = scn[u];
-          scn[u] = (kt >> 1) + 1 < nsb ? a_scales[dq_row[u] + (kt >> 1) + 1] : 0.0f;
-        }
-        const int q = threadIdx.x + u * NT, r = q / ACH, c = q % ACH;
-        const u32x4 raw = *reinterpret_cast<const u32x4*>(sb + r * AROWB + ((c ^ swz(r, ACH)) * 16));
-        bf16x8 lo8, hi8;
-        dequant16(raw, sc[u], lo8, hi8);
-        *reinterpret_cast<bf16x8*>(dq + r * ROWB + (((2 * c) ^ swz(r, CH)) * 16)) = lo8;
-        *reinterpret_cast<bf16x8*>(dq + r * ROWB + (((2 * c + 1) ^ swz(r, CH)) * 16)) = hi8;
+      for (int kk = 0; kk < 2; ++kk) {
+        const unsigned c = (unsigned)(((kk * 4 + fc) ^ swz(fr, CH)) * 16);
+        abase[st][kk] = l0 + st * STAGE_B + (wm * WTM + fr) * AROWB + c;
+        bbase[st][kk] = l0 + st * STAGE_B + A_BYTES + (wn * WTN + fr) * ROWB + c;
       }
-      // the bf16 tile is complete for every wave (its previous contents were
-      // retired by the barrier at the top of this step)
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      __builtin_amdgcn_s_barrier();
-    }
-#pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
-      bf16x8 bv[FN];
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int r = wn * WTN + j * 16 + fr, c = kk * 4 + fc;
-        bv[j] = *reinterpret_cast<const bf16x8*>(sb + A_BYTES + r * ROWB + ((c ^ swz(r, CH)) * 16));
-      }
-      bf16x8 av[FM];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int r = wm * WTM + i * 16 + fr, c = kk * 4 + fc;
-        av[i] = AFP8 ? *reinterpret_cast<const bf16x8*>(dq + r * ROWB + ((c ^ swz(r, CH)) * 16))
-                     : *reinterpret_cast<const bf16x8*>(sb + r * AROWB + ((c ^ swz(r, ACH)) * 16));
-      }
+    bf16x8 a0[FM], b0[FN], a1[FM], b1[FN];
+    auto read = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN], unsigned ab, unsigned bb) {
+      MOE_DS_READ_B128(av[0], ab, 0);
+      MOE_DS_READ_B128(av[1], ab, 2048);
+      MOE_DS_READ_B128(av[2], ab, 4096);
+      MOE_DS_READ_B128(av[3], ab, 6144);
+      MOE_DS_READ_B128(bv[0], bb, 0);
+      MOE_DS_READ_B128(bv[1], bb, 2048);
+      MOE_DS_READ_B128(bv[2], bb, 4096);
+      MOE_DS_READ_B128(bv[3], bb, 6144);
+      MOE_DS_READ_B128(bv[4], bb, 8192);
+      MOE_DS_READ_B128(bv[5], bb, 10240);
+      MOE_DS_READ_B128(bv[6], bb, 12288);
+      MOE_DS_READ_B128(bv[7], bb, 14336);
+    };
+    auto mma = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN]) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+    };
+    issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (KT > 1) issue(1, 1);
+    read(a0, b0, abase[0][0], bbase[0][0]);
+    for (int kt = 0; kt < KT; kt += 2) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int k2 = kt + u;  // stage k2 lives in buffer u
+        if (k2 < KT) {
+          read(a1, b1, abase[u][1], bbase[u][1]);
+          __builtin_amdgcn_sched_barrier(0);
+          asm volatile("s_waitcnt lgkmcnt(12)" ::: "memory");  // a0 / b0 (the older 12) landed
+          __builtin_amdgcn_sched_barrier(0);
+          mma(a0, b0);
+          __builtin_amdgcn_sched_barrier(0);
+          // this wave's reads of stage k2 and its DMA of stage k2 + 1 are done;
+          // the barrier makes that true for every wave
+          asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+          __builtin_amdgcn_sched_barrier(0);
+          if (k2 + 2 < KT) issue(k2 + 2, u);
+          if (k2 + 1 < KT) read(a0, b0, abase[u ^ 1][0], bbase[u ^ 1][0]);
+          __builtin_amdgcn_sched_barrier(0);
+          mma(a1, b1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  } else {
+  #pragma unroll
+    for (int st = 0; st < NS - 1; ++st)
+      if (st < KT) issue(st, st);
+    for (int kt = 0; kt < KT; ++kt) {
+      // this wave's stage kt landed once at most the NS-2 later stages are
+      // outstanding; the barrier then publishes every wave's DMA and retires
+      // all reads of the buffer reloaded next
+      if (kt + NS - 2 < KT)
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 2) * PER_WAVE) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if (kt + NS - 1 < KT) issue(kt + NS - 1, (kt + NS - 1) % NS);
+      const char* sb = lds + (kt % NS) * STAGE_B;
+      if (AFP8) {
+        const bool nb = kt > 0 && (kt & 1) == 0;  // a new 128-wide scale block starts
+  #pragma unroll
+        for (int u = 0; u < DQ_PER; ++u) {
+          if (nb) {
+            sc[u] = scn[u];
+            scn[u] = (kt >> 1) + 1 < nsb ? a_scales[dq_row[u] + (kt >> 1) + 1] : 0.0f;
+          }
+          const int q = threadIdx.x + u * NT, r = q / ACH, c = q % ACH;
+          const u32x4 raw = *reinterpret_cast<const u32x4*>(sb + r * AROWB + ((c ^ swz(r, ACH)) * 16));
+          bf16x8 lo8, hi8;
+          dequant16(raw, sc[u], lo8, hi8);
+          *reinterpret_cast<bf16x8*>(dq + r * ROWB + (((2 * c) ^ swz(r, CH)) * 16)) = lo8;
+          *reinterpret_cast<bf16x8*>(dq + r * ROWB + (((2 * c + 1) ^ swz(r, CH)) * 16)) = hi8;
+        }
+        // the bf16 tile is complete for every wave (its previous contents were
+        // retired by the barrier at the top of this step)
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+      }
+  #pragma unroll
+      for (int kk = 0; kk < BK / 32; ++kk) {
+        bf16x8 bv[FN];
+  #pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int r = wn * WTN + j * 16 + fr, c = kk * 4 + fc;
+          bv[j] = *reinterpret_cast<const bf16x8*>(sb + A_BYTES + r * ROWB + ((c ^ swz(r, CH)) * 16));
+        }
+        bf16x8 av[FM];
+  #pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int r = wm * WTM + i * 16 + fr, c = kk * 4 + fc;
+          av[i] = AFP8 ? *reinterpret_cast<const bf16x8*>(dq + r * ROWB + ((c ^ swz(r, CH)) * 16))
+                       : *reinterpret_cast<const bf16x8*>(sb + r * AROWB + ((c ^ swz(r, ACH)) * 16));
+        }
+  #pragma unroll
+        for (int i = 0; i < FM; ++i)
+  #pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+      }
     }
   }
 
@@ -307,7 +403,7 @@ int grouped_gemm_n_tiles(int N, bool swiglu) {
   return (N + per - 1) / per;
 }
 
-template <bool AFP8, int WM, int WN>
+template <bool AFP8, int WM, int WN, bool PIPE>
 static hipError_t launch_gg(const void* a, const float* a_scales, const void* ident_a, int ident_m,
                             const void* w0, const void* w1, const int32_t* offs, int G, int M, int N,
                             int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
@@ -317,11 +413,11 @@ static hipError_t launch_gg(const void* a, const float* a_scales, const void* id
   blocks = (blocks + 7) / 8 * 8;
   const dim3 grid((unsigned)blocks), blk(64 * WM * WN);
   if (swiglu)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, 64, 2, WM, WN>), grid, blk, 0, s, a,
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, 64, 2, WM, WN, PIPE>), grid, blk, 0, s, a,
                        a_scales, ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1, offs,
                        tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, 64, 2, WM, WN>), grid, blk, 0, s, a,
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, 64, 2, WM, WN, PIPE>), grid, blk, 0, s, a,
                        a_scales, ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0, offs,
                        tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
   return hipGetLastError();
@@ -340,13 +436,14 @@ hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const void*
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (M == 0 || N == 0 || G == 0) return hipSuccess;
-  // 16 waves of 64 x 64 accumulators; 8 waves of 64 x 128 measured within +-5%
-  // at the reference's expert shapes (same results)
+  // bf16 A: 8 waves of 64 x 128 accumulators with the software-pipelined K
+  // loop.  fp8 A (its dequantisation pass needs a barrier inside each K step):
+  // 16 waves of 64 x 64 with the plain loop.
   if (a_scales)
-    return launch_gg<true, 4, 4>(a, a_scales, ident_a, ident_m, w0, w1, offs, G, M, N, K, swiglu,
-                                 out, tile_start, s);
-  return launch_gg<false, 4, 4>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M, N, K, swiglu,
-                                out, tile_start, s);
+    return launch_gg<true, 4, 4, false>(a, a_scales, ident_a, ident_m, w0, w1, offs, G, M, N, K,
+                                        swiglu, out, tile_start, s);
+  return launch_gg<false, 4, 2, true>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M, N, K,
+                                      swiglu, out, tile_start, s);
 }
 
 }  // namespace moe
