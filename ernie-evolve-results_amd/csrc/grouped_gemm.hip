@@ -11,8 +11,8 @@
 //
 // Plan (the reference's plan_kernel builds per-group pointers for CUTLASS on
 // the device; here it is one scan): tile_start[g] = sum over g' < g of
-// ceil(m_g' / 256), on the device, so nothing waits for the host.  The grid
-// is sized by the bound sum ceil(m_g / 256) <= ceil(M / 256) + G; blocks past
+// ceil(m_g' / BM), on the device, so nothing waits for the host.  The grid
+// is sized by the bound sum ceil(m_g / BM) <= ceil(M / BM) + G; blocks past
 // the last tile return at once.
 //
 // Tiles: 256 rows x 256 weight rows, 64-wide K steps, staged in LDS by the
@@ -36,11 +36,11 @@
 
 namespace moe {
 
-constexpr int kGgBM = 256, kGgBN = 256;
+constexpr int kGgBN = 256;  // weight rows per tile (row tiles: 128 or 256, a template parameter)
 
 // One workgroup of 1024 threads: inclusive scan of per-group tile counts.
 __global__ __launch_bounds__(1024) void gg_plan_kernel(const int* __restrict__ offs, int G, int M,
-                                                       int* __restrict__ tile_start) {
+                                                       int bm, int* __restrict__ tile_start) {
   __shared__ int part[16];
   __shared__ int carry;
   if (threadIdx.x == 0) carry = 0;
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(1024) void gg_plan_kernel(const int* __restrict__ o
     if (g < G) {
       const int lo = g > 0 ? min(max(offs[g - 1], 0), M) : 0;
       const int hi = min(max(offs[g], 0), M);
-      tiles = hi > lo ? (hi - lo + kGgBM - 1) / kGgBM : 0;
+      tiles = hi > lo ? (hi - lo + bm - 1) / bm : 0;
     }
     // wave inclusive scan
     int v = tiles;
@@ -113,7 +113,7 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 #define MOE_DS_READ_B128(dst, addr, off) \
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(off))
 
-template <bool SWIGLU, bool AFP8, int BK, int NS, int WM, int WN, bool PIPE>
+template <bool SWIGLU, bool AFP8, int BK, int NS, int WM, int WN, bool PIPE, int BM>
 __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     const void* __restrict__ a_, const float* __restrict__ a_scales, const void* __restrict__ ident_,
     int ident_m, const __bf16* __restrict__ w0, const __bf16* __restrict__ w1,
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     int n_tiles, unsigned short* __restrict__ out) {
   // LDS rows: B (weights, bf16) BK*2 bytes; A BK*2 bytes (bf16) or BK bytes (fp8).
   // A DMA wave instruction moves 1 KB = 1024 / row-bytes rows.
-  constexpr int BM = kGgBM, BN = kGgBN;
+  constexpr int BN = kGgBN;
   constexpr int ROWB = BK * 2, CH = ROWB / 16, RPI = 1024 / ROWB;
   constexpr int AROWB = AFP8 ? BK : BK * 2, ACH = AROWB / 16, ARPI = 1024 / AROWB;
   constexpr int A_BYTES = BM * AROWB, STAGE_B = A_BYTES + BN * ROWB;
@@ -137,8 +137,8 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   static_assert(!AFP8 || BK == 64, "fp8 A: one 128-wide scale block spans two K steps");
   static_assert(!AFP8 || (BM * ACH) % NT == 0, "fp8 A: whole 16-byte chunks per thread per K step");
   static_assert(!SWIGLU || FN % 2 == 0, "swiglu: gate/up fragment pairs inside one wave");
-  static_assert(!PIPE || (!AFP8 && BK == 64 && NS == 2 && WM == 4 && WN == 2),
-                "pipelined loop: bf16 A, 2 stages of 64, 8 waves of 64 x 128");
+  static_assert(!PIPE || (!AFP8 && BK == 64 && NS == 2 && WM == 4 && WN == 2 && BM == 256),
+                "pipelined loop: bf16 A, 256-row tiles, 2 stages of 64, 8 waves of 64 x 128");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B + DQ_BYTES];
   char* const dq = lds + NS * STAGE_B;
   const char* a = (const char*)a_;
@@ -403,47 +403,53 @@ int grouped_gemm_n_tiles(int N, bool swiglu) {
   return (N + per - 1) / per;
 }
 
-template <bool AFP8, int WM, int WN, bool PIPE>
+template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS>
 static hipError_t launch_gg(const void* a, const float* a_scales, const void* ident_a, int ident_m,
                             const void* w0, const void* w1, const int32_t* offs, int G, int M, int N,
                             int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
+  hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, BM, tile_start);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (M == 0 || N == 0 || G == 0) return hipSuccess;
   const int n_tiles = grouped_gemm_n_tiles(N, swiglu);
-  const long long m_bound = ((long long)M + kGgBM - 1) / kGgBM + G;
+  const long long m_bound = ((long long)M + BM - 1) / BM + G;
   long long blocks = m_bound * n_tiles;
   blocks = (blocks + 7) / 8 * 8;
   const dim3 grid((unsigned)blocks), blk(64 * WM * WN);
   if (swiglu)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, 64, 2, WM, WN, PIPE>), grid, blk, 0, s, a,
-                       a_scales, ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1, offs,
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, 64, NS, WM, WN, PIPE, BM>), grid, blk, 0, s,
+                       a, a_scales, ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1, offs,
                        tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, 64, 2, WM, WN, PIPE>), grid, blk, 0, s, a,
-                       a_scales, ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0, offs,
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, 64, NS, WM, WN, PIPE, BM>), grid, blk, 0, s,
+                       a, a_scales, ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0, offs,
                        tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
   return hipGetLastError();
 }
 
 // tile_start: [G+1] ints of workspace.  offs: inclusive group ends (device).
 // a_scales == NULL: a is bf16.  Else a is e4m3fn bytes with one fp32 scale per
-// row and 128-wide K block ([M, K/128]).  BK = 64 with a 2-stage ring
-// measured fastest on MI355X at the reference's expert shapes (BK = 32 with
-// 3 or 4 stages: 8-13% slower, same results).
+// row and 128-wide K block ([M, K/128]).
 hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const void* ident_a,
                                int ident_m, const void* w0, const void* w1, const int32_t* offs,
                                int G, int M, int N, int K, bool swiglu, void* out,
                                int32_t* tile_start, hipStream_t s) {
-  hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, tile_start);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (M == 0 || N == 0 || G == 0) return hipSuccess;
-  // bf16 A: 8 waves of 64 x 128 accumulators with the software-pipelined K
-  // loop.  fp8 A (its dequantisation pass needs a barrier inside each K step):
-  // 16 waves of 64 x 64 with the plain loop.
+  // fp8 A (its dequantisation pass needs a barrier inside each K step): 256-row
+  // tiles, 16 waves of 64 x 64, the plain loop.
   if (a_scales)
-    return launch_gg<true, 4, 4, false>(a, a_scales, ident_a, ident_m, w0, w1, offs, G, M, N, K,
-                                        swiglu, out, tile_start, s);
-  return launch_gg<false, 4, 2, true>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M, N, K,
-                                      swiglu, out, tile_start, s);
+    return launch_gg<true, 4, 4, false, 256, 2>(a, a_scales, ident_a, ident_m, w0, w1, offs, G, M,
+                                                N, K, swiglu, out, tile_start, s);
+  // bf16 A with small groups (<= 320 rows on average, e.g. T = 1571-2048
+  // routed top-8 over 64 experts): the weights stream from HBM with little
+  // reuse, so 128-row tiles with a 3-stage ring (2 stages in flight) win --
+  // measured 7-16% faster at T = 1571, 10% slower at T = 8192.
+  if ((long long)M <= 320ll * G)
+    return launch_gg<false, 2, 8, false, 128, 3>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M,
+                                                 N, K, swiglu, out, tile_start, s);
+  // bf16 A, larger groups: 256-row tiles, 8 waves of 64 x 128 accumulators,
+  // the software-pipelined K loop.
+  return launch_gg<false, 4, 2, true, 256, 2>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M, N,
+                                              K, swiglu, out, tile_start, s);
 }
 
 }  // namespace moe

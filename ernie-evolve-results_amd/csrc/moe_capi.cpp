@@ -302,7 +302,8 @@ static int grouped_common(const void* a, const float* a_scales, const void* w0, 
   if (ws_bytes < need)
     return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws_bytes, need);
   if (!aligned16(ws)) return fail(MOE_ERR_ALIGNMENT, "workspace not 16-byte aligned");
-  const long long blocks = (((long long)M + 255) / 256 + G) *
+  // row tiles are 128 or 256 rows: bound by the 128-row count
+  const long long blocks = (((long long)M + 127) / 128 + G) *
                            moe::grouped_gemm_n_tiles(N, swiglu);
   if (blocks >= (1ll << 31)) return fail(MOE_ERR_UNSUPPORTED, "too many tiles (%lld)", blocks);
   return launched(moe::launch_grouped_gemm(a, fp8 ? a_scales : nullptr, ident_a, ident_m, w0, w1,
