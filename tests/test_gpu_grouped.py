@@ -71,6 +71,41 @@ def test_grouped_gemm_ragged(cuda, sizes, N, K):
     check_plain(got, a, w, np.cumsum(sizes))
 
 
+@pytest.mark.parametrize("sizes,N,K", [
+    ([700, 0, 900], 256, 64),      # large groups (pipelined K loop), a single K step
+    ([700, 0, 900], 200, 192),     # three K steps (odd), partial column tile
+    ([1200, 333], 512, 320),       # five K steps
+])
+def test_grouped_gemm_large_groups_odd_k_steps(cuda, sizes, N, K):
+    """More than 320 rows per group selects the 256-row tiles with the
+    software-pipelined K loop; its tail handles odd and single K-step
+    counts."""
+    a, w = make(sizes, N, K, seed=sum(sizes) + K)
+    offs = inclusive(sizes, cuda)
+    got = M.grouped_gemm(a.to(cuda), w.to(cuda), offs)
+    torch.cuda.synchronize()
+    check_plain(got, a, w, np.cumsum(sizes))
+
+
+def test_grouped_swiglu_large_groups_odd_k_steps(cuda):
+    sizes, N, K = [900, 500], 160, 192
+    g = torch.Generator().manual_seed(77)
+    a = torch.randn(sum(sizes), K, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(2, N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    wu = (torch.randn(2, N, K, generator=g) / K ** 0.5).to(torch.bfloat16)
+    offs_np = np.cumsum(sizes)
+    h = M.grouped_swiglu(a.to(cuda), wg.to(cuda), wu.to(cuda), inclusive(sizes, cuda))
+    torch.cuda.synchronize()
+    uu = O.grouped_gemm(a, wu, offs_np).double()
+    gg = O.grouped_gemm(a, wg, offs_np).double()
+    ref = O.grouped_swiglu(a, wg, wu, offs_np).double()
+    dg, du = acc_bound(a, wg, offs_np), acc_bound(a, wu, offs_np)
+    lim = 1.1 * dg * uu.abs() + torch.nn.functional.silu(gg).abs() * du + dg * du + \
+        (2.0 ** -8 + 2.0 ** -20) * ref.abs()
+    err = (h.double().cpu() - ref).abs()
+    assert bool((err <= lim + 1e-30).all()), float((err / (lim + 1e-30)).max())
+
+
 def test_grouped_gemm_leaves_rows_outside_groups(cuda):
     sizes = [33, 0, 70]
     a, w = make(sizes, 128, 128, seed=11, extra_rows=50)
