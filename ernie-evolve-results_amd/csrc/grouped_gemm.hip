@@ -180,6 +180,10 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
+  // A wave whose rows all lie past the group (the last, partial row tile of a
+  // group) still issues its share of the DMA and joins every barrier, but
+  // skips its fragment reads and MFMAs: its results are never stored.
+  const bool live = r0 + wm * WTM <= rlast;
   // logical 16-byte chunk c of an LDS row r sits at c ^ swz(r): the 16 rows
   // of one fragment read fall on distinct bank groups
   auto swz = [](int r, int ch) { return ch == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
@@ -290,6 +294,13 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     issue(0, 0);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     if (KT > 1) issue(1, 1);
+    if (!live) {
+      // DMA and barriers only, in the same order as the live loop below
+      for (int k2 = 0; k2 < KT; ++k2) {
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (k2 + 2 < KT) issue(k2 + 2, k2 & 1);
+      }
+    } else {
     read(a0, b0, abase[0][0], bbase[0][0]);
     for (int kt = 0; kt < KT; kt += 2) {
 #pragma unroll
@@ -313,6 +324,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
           __builtin_amdgcn_sched_barrier(0);
         }
       }
+    }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   } else {
@@ -349,6 +361,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
         __builtin_amdgcn_s_barrier();
       }
+      if (!live) continue;
   #pragma unroll
       for (int kk = 0; kk < BK / 32; ++kk) {
         bf16x8 bv[FN];
