@@ -12,7 +12,7 @@ per-stage times, the end-to-end HBM fraction, and the CPU oracle's rate on a
 bounded sample of the same workload (rank 0, N=1).
 
     python bench.py [--steps K] [--warmup W] [--config C4|C5|C2|C3] [--no-cpu]
-    python bench.py --layer [T ...]   # the drop-in run() at the reference's workloads
+    python bench.py --layer [T ...] [--layer-int8]   # the drop-in run() at the reference's workloads
 
 --layer times the reference entry point run() (route, dispatch, SwiGLU
 experts and shared expert on the grouped GEMM, combine) at the reference's
@@ -106,7 +106,7 @@ def cpu_baseline(c, sample_T):
 LAYER_MIX = {1571: 1, 2048: 1, 4096: 3, 4904: 1, 8192: 3}  # kernel.cu:133-136
 
 
-def layer_bench(Ts, steps, warmup, dispatch="bf16"):
+def layer_bench(Ts, steps, warmup, dispatch="bf16", experts="bf16"):
     """run() latency per T (HIP events around each call, median of `steps`)."""
     dev = torch.device("cuda:0")
     H, E, Ni, SNi = 8192, 64, 3584, 7168
@@ -124,7 +124,7 @@ def layer_bench(Ts, steps, warmup, dispatch="bf16"):
     for T in Ts:
         hs = r(1, T, H).to(torch.bfloat16)
         args = (hs, gw, bias, eg, eu, ed, sg, su, sd, 1e-6)
-        run = lambda: M.run(*args, dispatch=dispatch)
+        run = lambda: M.run(*args, dispatch=dispatch, experts=experts)
         for _ in range(warmup):
             run()
         torch.cuda.synchronize()
@@ -143,11 +143,12 @@ def layer_bench(Ts, steps, warmup, dispatch="bf16"):
         "metric": "reference run() layer latency (route+dispatch+SwiGLU experts+shared+combine)",
         "value": round(sum(LAYER_MIX.get(T, 1) * ms[T] for T in Ts), 4), "unit": "ms",
         "n_gpus": 1, "steps": steps, "warmup": warmup, "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 experts, bf16 shared expert" if experts == "int8" else "bf16",
         "data": "synthetic (seeded randn, the reference harness's distributions)",
         "config": {"workload": "kernel.cu run(): NE=64 H=8192 Ni=3584 SNi=7168 top-8; value = "
                                "sum over T of mix weight x latency",
-                   "dispatch": dispatch,
+                   "dispatch": dispatch, "experts": experts,
                    "mix": {str(T): LAYER_MIX.get(T, 1) for T in Ts}},
         "per_T_ms": {str(T): round(v, 4) for T, v in ms.items()},
         "reference_b200_mix_sum_ms": 35.92,
@@ -170,6 +171,8 @@ def main():
                     help="time run() at the reference's workload T values (default: its mix)")
     ap.add_argument("--layer-fp8", action="store_true",
                     help="with --layer: run(..., dispatch='fp8')")
+    ap.add_argument("--layer-int8", action="store_true",
+                    help="with --layer: run(..., experts='int8'), the reference's expert precision")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this path runs on one GPU only (no sharding, no collectives); "
@@ -178,7 +181,7 @@ def main():
 
     if args.layer is not None:
         layer_bench(args.layer or sorted(LAYER_MIX), max(args.steps // 2, 5), 2,
-                    "fp8" if args.layer_fp8 else "bf16")
+                    "fp8" if args.layer_fp8 else "bf16", "int8" if args.layer_int8 else "bf16")
         return
 
     c = CONFIGS[args.config]
@@ -263,7 +266,8 @@ def main():
         "metric": "routed tokens/sec + achieved HBM GB/s (% of peak) at DSV3 shape, 1 MI355X",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 experts, bf16 shared expert" if experts == "int8" else "bf16",
         "data": "synthetic (seeded randn inputs generated on the GPU)",
         "config": {"workload": "%s route+dispatch+combine: %s" % (c.name, c.description),
                    "T": c.T, "H": c.H, "E": c.E, "k": c.k, "fp8_dispatch": c.fp8},

@@ -103,6 +103,20 @@ __device__ __forceinline__ void dequant16(u32x4 raw, float s, bf16x8& lo8, bf16x
   }
 }
 
+// Accumulator type and one MFMA of the K loop: bf16 16x16x32 (fp32 acc) or
+// int8 16x16x64 (int32 acc, exact).  Both read 16 bytes per lane per operand.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+template <bool I8> struct AccOf { typedef f32x4 type; };
+template <> struct AccOf<true> { typedef i32x4 type; };
+template <bool I8>
+__device__ __forceinline__ typename AccOf<I8>::type mfma_step(bf16x8 a, bf16x8 b,
+                                                              typename AccOf<I8>::type c) {
+  if constexpr (I8)
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8((i32x4)a, (i32x4)b, c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
 // 32-bit LDS address of a __shared__ location, for inline-asm LDS reads.
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
@@ -113,17 +127,33 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 #define MOE_DS_READ_B128(dst, addr, off) \
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(off))
 
-template <bool SWIGLU, bool AFP8, int BK, int NS, int WM, int WN, bool PIPE, int BM>
+// Row / column scales of the int8 operands (unused by the bf16 and fp8 paths).
+struct I8Scales {
+  const float* a;      // [M] per row of a, or indexed through a_idx
+  const int* a_idx;    // NULL, or [M]: row r of a uses a[a_idx[r]]
+  const float* ident;  // [ident_m] per row of ident_a
+  const float* w0;     // [G, N] per weight row of w0
+  const float* w1;     // [G, N] per weight row of w1 (SwiGLU up)
+};
+
+template <bool SWIGLU, bool AFP8, int BK, int NS, int WM, int WN, bool PIPE, int BM, bool I8>
 __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     const void* __restrict__ a_, const float* __restrict__ a_scales, const void* __restrict__ ident_,
-    int ident_m, const __bf16* __restrict__ w0, const __bf16* __restrict__ w1,
+    int ident_m, const void* __restrict__ w0_, const void* __restrict__ w1_,
     const int* __restrict__ offs, const int* __restrict__ tile_start, int G, int M, int N, int K,
-    int n_tiles, unsigned short* __restrict__ out) {
-  // LDS rows: B (weights, bf16) BK*2 bytes; A BK*2 bytes (bf16) or BK bytes (fp8).
-  // A DMA wave instruction moves 1 KB = 1024 / row-bytes rows.
+    int n_tiles, unsigned short* __restrict__ out, I8Scales i8s) {
+  // LDS rows: B (weights) BK*WEL bytes; A BK*2 bytes (bf16) or BK bytes (fp8,
+  // int8).  bf16 steps are 64 wide, int8 steps 128 wide: 128-byte rows either
+  // way.  A DMA wave instruction moves 1 KB = 1024 / row-bytes rows.
   constexpr int BN = kGgBN;
-  constexpr int ROWB = BK * 2, CH = ROWB / 16, RPI = 1024 / ROWB;
-  constexpr int AROWB = AFP8 ? BK : BK * 2, ACH = AROWB / 16, ARPI = 1024 / AROWB;
+  constexpr int WEL = I8 ? 1 : 2;  // bytes per weight element
+  constexpr int ROWB = BK * WEL, CH = ROWB / 16, RPI = 1024 / ROWB;
+  constexpr int AROWB = (AFP8 || I8) ? BK : BK * 2, ACH = AROWB / 16, ARPI = 1024 / AROWB;
+  // MFMA depth: v_mfma_f32_16x16x32_bf16 or v_mfma_i32_16x16x64_i8; both
+  // take 16 bytes per lane with the same lane -> (row, K chunk) layout.
+  constexpr int KSUB = I8 ? 64 : 32;
+  const char* const w0 = (const char*)w0_;
+  const char* const w1 = (const char*)w1_;
   constexpr int A_BYTES = BM * AROWB, STAGE_B = A_BYTES + BN * ROWB;
   // fp8 A: the DMA stages hold the e4m3fn bytes; each K step they are
   // dequantised once, cooperatively, into one bf16 tile (BM x BK) that the
@@ -132,18 +162,20 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int A_INST = BM / ARPI, B_INST = BN / RPI, PER_WAVE = (A_INST + B_INST) / NW;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
-  static_assert(BK == 32 || BK == 64, "K step of one or two MFMA depths");
+  static_assert(I8 ? BK == 128 : (BK == 32 || BK == 64), "K step of one or two MFMA depths");
+  static_assert(!(I8 && AFP8), "int8 and fp8 A are separate paths");
   static_assert((A_INST + B_INST) % NW == 0, "every wave issues the same number of loads");
   static_assert(!AFP8 || BK == 64, "fp8 A: one 128-wide scale block spans two K steps");
   static_assert(!AFP8 || (BM * ACH) % NT == 0, "fp8 A: whole 16-byte chunks per thread per K step");
   static_assert(!SWIGLU || FN % 2 == 0, "swiglu: gate/up fragment pairs inside one wave");
-  static_assert(!PIPE || (!AFP8 && BK == 64 && NS == 2 && WM == 4 && WN == 2 && BM == 256),
-                "pipelined loop: bf16 A, 256-row tiles, 2 stages of 64, 8 waves of 64 x 128");
+  static_assert(!PIPE || (!AFP8 && ROWB == 128 && NS == 2 && WM == 4 && WN == 2 && BM == 256),
+                "pipelined loop: bf16 / int8 A, 256-row tiles, 2 stages of 128-byte rows, "
+                "8 waves of 64 x 128");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B + DQ_BYTES];
   char* const dq = lds + NS * STAGE_B;
   const char* a = (const char*)a_;
   const char* ident_a = (const char*)ident_;
-  constexpr int AEL = AFP8 ? 1 : 2;  // bytes per A element
+  constexpr int AEL = (AFP8 || I8) ? 1 : 2;  // bytes per A element
 
   // XCD-aware order: gridDim.x is a multiple of 8, hardware block b runs on
   // XCD b % 8; logical tiles [x*nb/8, (x+1)*nb/8) all run on XCD x.
@@ -187,7 +219,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   // logical 16-byte chunk c of an LDS row r sits at c ^ swz(r): the 16 rows
   // of one fragment read fall on distinct bank groups
   auto swz = [](int r, int ch) { return ch == 8 ? (r >> 1) & 7 : (r >> 2) & 3; };
-  const long long wbase = (long long)g * N * K;
+  const long long wbase = (long long)g * N * K * WEL;  // bytes
 
   // DMA sources (bytes) and the byte advance per K step of each instruction
   const char* src[PER_WAVE];
@@ -205,7 +237,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     } else {
       const int r = (gi - A_INST) * RPI + lane / CH, p = lane % CH;
       int wrow;
-      const __bf16* wsrc = w0;
+      const char* wsrc = w0;
       if (SWIGLU) {
         const int f = r >> 4;
         wrow = nt * (BN / 2) + (f >> 1) * 16 + (r & 15);
@@ -214,8 +246,8 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
         wrow = nt * BN + r;
       }
       wrow = min(wrow, N - 1);
-      src[q] = (const char*)(wsrc + wbase + (long long)wrow * K) + (p ^ swz(r, CH)) * 16;
-      kstep[q] = BK * 2;
+      src[q] = wsrc + wbase + (long long)wrow * K * WEL + (p ^ swz(r, CH)) * 16;
+      kstep[q] = BK * WEL;
     }
   }
   auto issue = [&](int kt, int st) {
@@ -244,11 +276,12 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     scn[u] = AFP8 && nsb > 1 ? a_scales[dq_row[u] + 1] : 0.0f;
   }
 
-  f32x4 acc[FM][FN];
+  using AccV = typename AccOf<I8>::type;
+  AccV acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < FN; ++j) acc[i][j] = AccV{0, 0, 0, 0};
 
   const int KT = K / BK;
   if constexpr (PIPE) {
@@ -289,7 +322,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = mfma_step<I8>(av[i], bv[j], acc[i][j]);
     };
     issue(0, 0);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
@@ -363,7 +396,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
       }
       if (!live) continue;
   #pragma unroll
-      for (int kk = 0; kk < BK / 32; ++kk) {
+      for (int kk = 0; kk < BK / KSUB; ++kk) {
         bf16x8 bv[FN];
   #pragma unroll
         for (int j = 0; j < FN; ++j) {
@@ -381,31 +414,59 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
         for (int i = 0; i < FM; ++i)
   #pragma unroll
           for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bv[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = mfma_step<I8>(av[i], bv[j], acc[i][j]);
       }
     }
   }
 
   // Epilogue: lane holds rows (lane>>4)*4 + r, column lane & 15 of each 16x16 tile.
+  // int8: value = float(acc) * (row scale * column scale), in that order.
   const int ldo = N;
+  float cs0[FN], cs1[FN];  // int8 column scales of this lane's columns
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    cs0[j] = cs1[j] = 1.0f;
+    if constexpr (I8) {
+      const int col = SWIGLU ? nt * (BN / 2) + (wn * FN + (j & ~1)) / 2 * 16 + (lane & 15)
+                             : nt * BN + wn * WTN + j * 16 + (lane & 15);
+      if (col < N) {
+        cs0[j] = i8s.w0[(long long)g * N + col];
+        if (SWIGLU) cs1[j] = i8s.w1[(long long)g * N + col];
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = r0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
       if (row > rlast) continue;
+      float rs = 1.0f;
+      if constexpr (I8)
+        rs = ident ? i8s.ident[row - gs] : i8s.a[i8s.a_idx ? i8s.a_idx[row] : row];
       unsigned short* orow = out + (long long)row * ldo;
       if (SWIGLU) {
 #pragma unroll
         for (int j = 0; j < FN; j += 2) {
           const int col = nt * (BN / 2) + (wn * FN + j) / 2 * 16 + (lane & 15);
-          if (col < N) orow[col] = (unsigned short)f2bf(swiglu(acc[i][j][r], acc[i][j + 1][r]));
+          float gv, uv;
+          if constexpr (I8) {
+            gv = (float)acc[i][j][r] * (rs * cs0[j]);
+            uv = (float)acc[i][j + 1][r] * (rs * cs1[j]);
+          } else {
+            gv = acc[i][j][r];
+            uv = acc[i][j + 1][r];
+          }
+          if (col < N) orow[col] = (unsigned short)f2bf(swiglu(gv, uv));
         }
       } else {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
           const int col = nt * BN + wn * WTN + j * 16 + (lane & 15);
-          if (col < N) orow[col] = (unsigned short)f2bf(acc[i][j][r]);
+          float v;
+          if constexpr (I8) v = (float)acc[i][j][r] * (rs * cs0[j]);
+          else v = acc[i][j][r];
+          if (col < N) orow[col] = (unsigned short)f2bf(v);
         }
       }
     }
@@ -416,10 +477,12 @@ int grouped_gemm_n_tiles(int N, bool swiglu) {
   return (N + per - 1) / per;
 }
 
-template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS>
+template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS, bool I8 = false>
 static hipError_t launch_gg(const void* a, const float* a_scales, const void* ident_a, int ident_m,
                             const void* w0, const void* w1, const int32_t* offs, int G, int M, int N,
-                            int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
+                            int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s,
+                            I8Scales i8s = I8Scales{}) {
+  constexpr int BK = I8 ? 128 : 64;
   hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, BM, tile_start);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -430,13 +493,13 @@ static hipError_t launch_gg(const void* a, const float* a_scales, const void* id
   blocks = (blocks + 7) / 8 * 8;
   const dim3 grid((unsigned)blocks), blk(64 * WM * WN);
   if (swiglu)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, 64, NS, WM, WN, PIPE, BM>), grid, blk, 0, s,
-                       a, a_scales, ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w1, offs,
-                       tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, BK, NS, WM, WN, PIPE, BM, I8>), grid, blk,
+                       0, s, a, a_scales, ident_a, ident_m, w0, w1, offs, tile_start, G, M, N, K,
+                       n_tiles, (unsigned short*)out, i8s);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, 64, NS, WM, WN, PIPE, BM>), grid, blk, 0, s,
-                       a, a_scales, ident_a, ident_m, (const __bf16*)w0, (const __bf16*)w0, offs,
-                       tile_start, G, M, N, K, n_tiles, (unsigned short*)out);
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, BK, NS, WM, WN, PIPE, BM, I8>), grid, blk,
+                       0, s, a, a_scales, ident_a, ident_m, w0, w0, offs, tile_start, G, M, N, K,
+                       n_tiles, (unsigned short*)out, i8s);
   return hipGetLastError();
 }
 
@@ -463,6 +526,21 @@ hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const void*
   // the software-pipelined K loop.
   return launch_gg<false, 4, 2, true, 256, 2>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M, N,
                                               K, swiglu, out, tile_start, s);
+}
+
+// int8 A and weights, int32 accumulation, 128-wide K steps: the same tile
+// choice as bf16 (the LDS rows are 128 bytes in both).
+hipError_t launch_grouped_gemm_i8(const void* a, const float* a_rs, const int32_t* a_rs_idx,
+                                  const void* ident_a, const float* ident_rs, int ident_m,
+                                  const void* w0, const float* w0s, const void* w1,
+                                  const float* w1s, const int32_t* offs, int G, int M, int N, int K,
+                                  bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
+  const I8Scales sc{a_rs, a_rs_idx, ident_rs, w0s, swiglu ? w1s : w0s};
+  if ((long long)M <= 320ll * G)
+    return launch_gg<false, 2, 8, false, 128, 3, true>(a, nullptr, ident_a, ident_m, w0, w1, offs,
+                                                       G, M, N, K, swiglu, out, tile_start, s, sc);
+  return launch_gg<false, 4, 2, true, 256, 2, true>(a, nullptr, ident_a, ident_m, w0, w1, offs, G,
+                                                    M, N, K, swiglu, out, tile_start, s, sc);
 }
 
 }  // namespace moe

@@ -8,6 +8,7 @@
 // buffer whose size moe_*_workspace_bytes reports).
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -338,6 +339,86 @@ int moe_grouped_swiglu_fp8(const void* a, const float* a_scales, const void* wg,
                            size_t ws_bytes, void* stream) {
   return grouped_common(a, a_scales, wg, wu, offs, G, M, N, K, nullptr, 0, h, ws, ws_bytes,
                         stream, true, true);
+}
+
+static int grouped_i8_common(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+                             const int8_t* w0, const float* w0s, const int8_t* w1,
+                             const float* w1s, const int32_t* offs, int G, int M, int N, int K,
+                             const int8_t* ident_a, const float* ident_scales, int ident_m,
+                             void* out, void* ws, size_t ws_bytes, void* stream, bool swiglu) {
+  if (G < 1 || G > 65536) return fail(MOE_ERR_INVALID_ARG, "G=%d not in [1, 65536]", G);
+  if (M < 0 || N < 1 || K < 1) return fail(MOE_ERR_INVALID_ARG, "M=%d, N=%d, K=%d", M, N, K);
+  if (K % 128 != 0) return fail(MOE_ERR_UNSUPPORTED, "int8 K=%d is not a multiple of 128", K);
+  if (ident_m < 0) return fail(MOE_ERR_INVALID_ARG, "ident_m=%d < 0", ident_m);
+  if (!offs || !ws) return fail(MOE_ERR_NULL_POINTER, "offs and ws are required");
+  if (M > 0 && (!a || !a_scales || !w0 || !w0s || !w1 || !w1s || !out))
+    return fail(MOE_ERR_NULL_POINTER, "a, the weights, their scales and the output are required");
+  if (ident_m > 0 && (!ident_a || !ident_scales))
+    return fail(MOE_ERR_NULL_POINTER, "ident_m > 0 needs ident_a and ident_scales");
+  if ((a && !aligned16(a)) || (w0 && !aligned16(w0)) || (w1 && !aligned16(w1)) ||
+      (ident_a && !aligned16(ident_a)))
+    return fail(MOE_ERR_ALIGNMENT, "a, ident_a and the weights must be 16-byte aligned");
+  if ((a_scales && ((uintptr_t)a_scales & 3u)) || (w0s && ((uintptr_t)w0s & 3u)) ||
+      (w1s && ((uintptr_t)w1s & 3u)) || (ident_scales && ((uintptr_t)ident_scales & 3u)) ||
+      (a_scale_idx && ((uintptr_t)a_scale_idx & 3u)))
+    return fail(MOE_ERR_ALIGNMENT, "scales and a_scale_idx must be 4-byte aligned");
+  if ((long long)M * K >= (1ll << 40) || (long long)G * N * K >= (1ll << 40) ||
+      (long long)G * N >= (1ll << 31))
+    return fail(MOE_ERR_UNSUPPORTED, "operands too large");
+  const size_t need = moe_grouped_gemm_workspace_bytes(G);
+  if (ws_bytes < need)
+    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws_bytes, need);
+  if (!aligned16(ws)) return fail(MOE_ERR_ALIGNMENT, "workspace not 16-byte aligned");
+  const long long blocks = (((long long)M + 127) / 128 + G) *
+                           moe::grouped_gemm_n_tiles(N, swiglu);
+  if (blocks >= (1ll << 31)) return fail(MOE_ERR_UNSUPPORTED, "too many tiles (%lld)", blocks);
+  return launched(moe::launch_grouped_gemm_i8(a, a_scales, a_scale_idx, ident_a, ident_scales,
+                                              ident_m, w0, w0s, w1, w1s, offs, G, M, N, K, swiglu,
+                                              out, (int32_t*)ws, (hipStream_t)stream),
+                  swiglu ? "grouped_swiglu_i8" : "grouped_gemm_i8");
+}
+
+int moe_grouped_gemm_i8(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+                        const int8_t* w, const float* w_scales, const int32_t* offs, int G, int M,
+                        int N, int K, const int8_t* ident_a, const float* ident_scales,
+                        int ident_m, void* out, void* ws, size_t ws_bytes, void* stream) {
+  return grouped_i8_common(a, a_scales, a_scale_idx, w, w_scales, w, w_scales, offs, G, M, N, K,
+                           ident_a, ident_scales, ident_m, out, ws, ws_bytes, stream, false);
+}
+
+int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+                          const int8_t* wg, const float* wg_scales, const int8_t* wu,
+                          const float* wu_scales, const int32_t* offs, int G, int M, int N, int K,
+                          const int8_t* ident_a, const float* ident_scales, int ident_m, void* h,
+                          void* ws, size_t ws_bytes, void* stream) {
+  return grouped_i8_common(a, a_scales, a_scale_idx, wg, wg_scales, wu, wu_scales, offs, G, M, N,
+                           K, ident_a, ident_scales, ident_m, h, ws, ws_bytes, stream, true);
+}
+
+int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float scale_mul,
+                      int group_rows, const int32_t* group_counts, int8_t* q, float* scales,
+                      void* stream) {
+  if (R < 0 || K < 1) return fail(MOE_ERR_INVALID_ARG, "R=%lld, K=%d", R, K);
+  if (R >= (1ll << 31)) return fail(MOE_ERR_UNSUPPORTED, "R=%lld rows exceeds the grid", R);
+  if (hadamard != 0 && hadamard != 128)
+    return fail(MOE_ERR_INVALID_ARG, "hadamard=%d (0 or 128)", hadamard);
+  if (K % (hadamard ? 128 : 16) != 0)
+    return fail(MOE_ERR_UNSUPPORTED, "K=%d is not a multiple of %d", K, hadamard ? 128 : 16);
+  if (K > moe::quant_rows_max_k())
+    return fail(MOE_ERR_UNSUPPORTED, "K=%d > %d", K, moe::quant_rows_max_k());
+  if (!(scale_mul > 0.0f) || !std::isfinite(scale_mul))
+    return fail(MOE_ERR_INVALID_ARG, "scale_mul must be finite and > 0");
+  if (group_counts && group_rows < 1)
+    return fail(MOE_ERR_INVALID_ARG, "group_rows=%d with group_counts", group_rows);
+  if (R > 0 && (!x || !q || !scales))
+    return fail(MOE_ERR_NULL_POINTER, "x, q and scales are required");
+  if ((x && !aligned16(x)) || (q && !aligned16(q)) || (scales && ((uintptr_t)scales & 3u)) ||
+      (group_counts && ((uintptr_t)group_counts & 3u)))
+    return fail(MOE_ERR_ALIGNMENT, "x and q must be 16-byte aligned, scales 4-byte aligned");
+  return launched(moe::launch_quant_rows_i8((const __bf16*)x, R, K, hadamard != 0, scale_mul,
+                                            group_rows, group_counts, (signed char*)q, scales,
+                                            (hipStream_t)stream),
+                  "quant_rows_i8");
 }
 
 }  // extern "C"

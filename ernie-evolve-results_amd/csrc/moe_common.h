@@ -67,6 +67,19 @@ hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const void*
                                int G, int M, int N, int K, bool swiglu, void* out,
                                int32_t* tile_start, hipStream_t s);
 
+// int8 grouped GEMM: a / ident_a / w0 / w1 int8, per-row scales a_rs (through
+// a_rs_idx when not NULL) and ident_rs, per-weight-row scales w0s / w1s [G, N].
+hipError_t launch_grouped_gemm_i8(const void* a, const float* a_rs, const int32_t* a_rs_idx,
+                                  const void* ident_a, const float* ident_rs, int ident_m,
+                                  const void* w0, const float* w0s, const void* w1,
+                                  const float* w1s, const int32_t* offs, int G, int M, int N, int K,
+                                  bool swiglu, void* out, int32_t* tile_start, hipStream_t s);
+// Per-row int8 quantisation, optional 128-block Walsh-Hadamard rotation.
+int quant_rows_max_k();
+hipError_t launch_quant_rows_i8(const __bf16* x, long long R, int K, bool had, float scale_mul,
+                                int group_rows, const int* counts, signed char* q, float* s,
+                                hipStream_t st);
+
 // Experts per lane of the scoring kernel for (E, scoring, n_group).
 int topk_lane_width(int E, int scoring, int n_group);
 

@@ -32,7 +32,8 @@ EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
            "moe_router_gemm", "moe_topk", "moe_route", "moe_offsets",
            "moe_permute_workspace_bytes", "moe_permute", "moe_combine",
            "moe_grouped_gemm_workspace_bytes", "moe_grouped_gemm", "moe_grouped_swiglu",
-           "moe_grouped_gemm_fp8", "moe_grouped_swiglu_fp8"]
+           "moe_grouped_gemm_fp8", "moe_grouped_swiglu_fp8", "moe_quant_rows_i8",
+           "moe_grouped_gemm_i8", "moe_grouped_swiglu_i8"]
 
 
 class MoeError(RuntimeError):
@@ -94,6 +95,14 @@ def lib():
         L.moe_grouped_gemm_fp8.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _Z, _P]
         L.moe_grouped_swiglu_fp8.restype = _I
         L.moe_grouped_swiglu_fp8.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _Z, _P]
+        L.moe_quant_rows_i8.restype = _I
+        L.moe_quant_rows_i8.argtypes = [_P, ctypes.c_longlong, _I, _I, _F, _I, _P, _P, _P, _P]
+        L.moe_grouped_gemm_i8.restype = _I
+        L.moe_grouped_gemm_i8.argtypes = [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P,
+                                          _P, _Z, _P]
+        L.moe_grouped_swiglu_i8.restype = _I
+        L.moe_grouped_swiglu_i8.argtypes = [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P,
+                                            _I, _P, _P, _Z, _P]
         _lib = L
     return _lib
 
@@ -323,6 +332,79 @@ def grouped_swiglu_fp8(a, a_scales, wg, wu, offs, out=None):
     return out
 
 
+def quant_rows_i8(x, hadamard=0, scale_mul=1.0, group_rows=0, group_counts=None, q=None,
+                  scales=None):
+    """Per-row symmetric int8 of bf16 rows x [..., K] (the reference's
+    xquant / hquant / wquant, moe_wq.h:150-188): optional 128-block
+    Walsh-Hadamard rotation, q = clamp(rint(v * 127 / amax), +-127),
+    scales = amax / 127 * scale_mul.  With group_counts, rows of groups with
+    count 0 are skipped.  Returns (q int8, scales fp32 [rows])."""
+    _dev(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise RuntimeError("x must be bf16")
+    K = x.shape[-1]
+    R = x.numel() // K if K else 0
+    if q is None:
+        q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    if scales is None:
+        scales = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    if group_counts is not None:
+        _dev(group_counts, "group_counts")
+    _check(lib().moe_quant_rows_i8(_ptr(x), R, K, int(hadamard), float(scale_mul),
+                                   int(group_rows), _ptr(group_counts), _ptr(q), _ptr(scales),
+                                   _stream(x)))
+    return q, scales
+
+
+def _i8_args(a, a_scales, offs, a_scale_idx, ident_a, ident_scales, ident_m):
+    for t, n in ((a, "a"), (a_scales, "a_scales"), (offs, "offs")):
+        _dev(t, n)
+    if a.dtype != torch.int8:
+        raise RuntimeError("a must be int8")
+    if offs.dtype != torch.int32:
+        raise RuntimeError("offs must be int32 inclusive group ends")
+    if ident_m and (ident_a is None or ident_scales is None):
+        raise RuntimeError("ident_m > 0 needs ident_a and ident_scales")
+    return torch.empty(max(lib().moe_grouped_gemm_workspace_bytes(offs.numel()), 256),
+                       dtype=torch.uint8, device=a.device)
+
+
+def grouped_gemm_i8(a, a_scales, w, w_scales, offs, a_scale_idx=None, ident_a=None,
+                    ident_scales=None, ident_m=0, out=None):
+    """int8 grouped GEMM (the reference's int8 grouped_mm, moe_int8.h:27-45):
+    out[r, n] = bf16(float(a[r] . w[g, n]) * (sa(r) * w_scales[g, n])), exact
+    int32 accumulation; sa(r) = a_scales[a_scale_idx[r]] (or a_scales[r]).
+    a [M,K] int8, w [G,N,K] int8, w_scales [G,N] fp32; returns bf16 [M,N]."""
+    ws = _i8_args(a, a_scales, offs, a_scale_idx, ident_a, ident_scales, ident_m)
+    G, N, K = w.shape
+    M = a.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    _check(lib().moe_grouped_gemm_i8(_ptr(a), _ptr(a_scales), _ptr(a_scale_idx), _ptr(w),
+                                     _ptr(w_scales), _ptr(offs), G, M, N, K, _ptr(ident_a),
+                                     _ptr(ident_scales), int(ident_m), _ptr(out), _ptr(ws),
+                                     ws.numel(), _stream(a)))
+    return out
+
+
+def grouped_swiglu_i8(a, a_scales, wg, wg_scales, wu, wu_scales, offs, a_scale_idx=None,
+                      ident_a=None, ident_scales=None, ident_m=0, out=None):
+    """int8 SwiGLU grouped GEMM: h = bf16(silu(g) * u), g and u the dequantised
+    int8 products of a with wg[g] and wu[g] (see grouped_gemm_i8)."""
+    ws = _i8_args(a, a_scales, offs, a_scale_idx, ident_a, ident_scales, ident_m)
+    if wg.shape != wu.shape:
+        raise RuntimeError("gate and up weights must have one shape")
+    G, N, K = wg.shape
+    M = a.shape[0]
+    if out is None:
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    _check(lib().moe_grouped_swiglu_i8(_ptr(a), _ptr(a_scales), _ptr(a_scale_idx), _ptr(wg),
+                                       _ptr(wg_scales), _ptr(wu), _ptr(wu_scales), _ptr(offs), G,
+                                       M, N, K, _ptr(ident_a), _ptr(ident_scales), int(ident_m),
+                                       _ptr(out), _ptr(ws), ws.numel(), _stream(a)))
+    return out
+
+
 def route_dispatch_combine(x, w, bias, y, k, cfg: RouteCfg, fp8=False):
     """The whole path for one batch: route, permute (bf16 or fp8), combine y."""
     logits, ids, wts, counts = route(x, w, bias, k, cfg)
@@ -340,7 +422,7 @@ REF_NE, REF_TOPK = 64, 8  # K:1582-1583
 
 def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, expert_up_proj,
         expert_down_proj, shared_gate_proj, shared_up_proj, shared_down_proj, norm_min, *,
-        dispatch="bf16"):
+        dispatch="bf16", experts="bf16"):
     """Drop-in for the reference's run() (K:4067-4077): returns
     (out [B,S,H] bf16, router_logits [T,64] fp32).
 
@@ -356,9 +438,21 @@ def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, e
       combine   out = shared + sum_j w_j y[pair_row]  (K:2365-2428).
     dispatch="fp8" (keyword only, not in the reference signature) permutes the
     routed rows to e4m3fn with per-128 scales and dequantises them inside the
-    expert gate+up GEMM's A load."""
+    expert gate+up GEMM's A load.
+
+    experts="int8" (keyword only) runs the routed experts the way the
+    reference's own run() does (int8 experts, kernel.cu:61-66): x quantised
+    per token, each routed expert's weights per output row (only experts that
+    received rows), the gate+up products dequantised in the GEMM epilogue
+    before silu*mul, h rotated by 128-point Walsh-Hadamard blocks and
+    quantised per row, the down weights rotated the same way (1/128 folded
+    into their scales), and an int8 down GEMM.  The shared expert stays bf16."""
     if dispatch not in ("bf16", "fp8"):
         raise RuntimeError("dispatch must be 'bf16' or 'fp8'")
+    if experts not in ("bf16", "int8"):
+        raise RuntimeError("experts must be 'bf16' or 'int8'")
+    if experts == "int8" and dispatch != "bf16":
+        raise RuntimeError("experts='int8' dispatches int8 rows; dispatch must stay 'bf16'")
     B, S, H = hidden_states.shape
     T = B * S
     x = hidden_states.reshape(T, H)
@@ -367,21 +461,49 @@ def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, e
     cfg = RouteCfg(SCORING_SOFTMAX_BIAS, True, 1, 1, 1.0, float(norm_min))
     logits, ids, wts, _ = route(x, gate_weight.float().contiguous(),
                                 e_score_correction_bias.float().contiguous(), REF_TOPK, cfg)
-    p = permute(x, ids, E, fp8=dispatch == "fp8")
-    ends = p["offsets"][1:]  # inclusive group ends (moe_gemm.h:66-69)
-    if dispatch == "fp8":
-        h = grouped_swiglu_fp8(p["xg"], p["scales"], expert_gate_proj.contiguous(),
-                               expert_up_proj.contiguous(), ends)
+    if experts == "int8":
+        y, p = _experts_int8(x, ids, E, expert_gate_proj.contiguous(),
+                             expert_up_proj.contiguous(), expert_down_proj.contiguous())
     else:
-        h = grouped_swiglu(p["xg"], expert_gate_proj.contiguous(), expert_up_proj.contiguous(),
-                           ends)
-    y = grouped_gemm(h, expert_down_proj.contiguous(), ends)
+        y, p = _experts_bf16(x, ids, E, dispatch, expert_gate_proj.contiguous(),
+                             expert_up_proj.contiguous(), expert_down_proj.contiguous())
     dense = torch.full((1,), T, dtype=torch.int32, device=x.device)
     sh_h = grouped_swiglu(x.contiguous(), shared_gate_proj.contiguous().unsqueeze(0),
                           shared_up_proj.contiguous().unsqueeze(0), dense)
     sh = grouped_gemm(sh_h, shared_down_proj.contiguous().unsqueeze(0), dense)
     out = combine(y, p["pair_row"], wts, shared=sh)
     return out.view(B, S, H), logits
+
+
+def _experts_bf16(x, ids, E, dispatch, wg, wu, wd):
+    p = permute(x, ids, E, fp8=dispatch == "fp8")
+    ends = p["offsets"][1:]  # inclusive group ends (moe_gemm.h:66-69)
+    if dispatch == "fp8":
+        h = grouped_swiglu_fp8(p["xg"], p["scales"], wg, wu, ends)
+    else:
+        h = grouped_swiglu(p["xg"], wg, wu, ends)
+    return grouped_gemm(h, wd, ends), p
+
+
+def _experts_int8(x, ids, E, wg, wu, wd):
+    """The routed experts in int8 (see run): returns (y [T*k, H] bf16, permute
+    dict)."""
+    T, H = x.shape
+    Ni = wg.shape[1]
+    xq, xs = quant_rows_i8(x)
+    # the int8 rows travel through the row permute as 2-byte units
+    p = permute(xq.view(torch.bfloat16), ids, E)
+    xg = p["xg"].view(torch.int8)
+    counts = p["counts"]
+    ends = p["offsets"][1:]
+    wgq, wgs = quant_rows_i8(wg, group_rows=Ni, group_counts=counts)
+    wuq, wus = quant_rows_i8(wu, group_rows=Ni, group_counts=counts)
+    wdq, wds = quant_rows_i8(wd, hadamard=128, scale_mul=1.0 / 128, group_rows=H,
+                             group_counts=counts)
+    h = grouped_swiglu_i8(xg, xs, wgq, wgs, wuq, wus, ends, a_scale_idx=p["row_token"],
+                          ident_a=xq, ident_scales=xs, ident_m=T)
+    hq, hs = quant_rows_i8(h, hadamard=128)
+    return grouped_gemm_i8(hq, hs, wdq, wds, ends), p
 
 
 # ---------------------------------------------------------------------------

@@ -179,6 +179,41 @@ int moe_grouped_swiglu_fp8(const void* a, const float* a_scales, const void* wg,
                            const int32_t* offs, int G, int M, int N, int K, void* h, void* ws,
                            size_t ws_bytes, void* stream);
 
+/* int8 expert path (the reference's int8 experts: xquant / hquant / wquant,
+ * kernel.cu:61-66 and kernel.cu:125-129, the int8 grouped GEMMs
+ * moe_int8.h:27-45 / moe_int8.cu:391-393, the quantiser moe_wq.h:150-188).
+ *
+ * Per-row symmetric int8 quantisation of R rows of K bf16 values:
+ *   v = the row (hadamard == 128: rotated in blocks of 128 along the row by the
+ *       unnormalised Walsh-Hadamard transform, butterfly stages 1, 2, ..., 64),
+ *   q = clamp(rint(v * (127 / max|v|)), -127, 127), 0 for an all-zero row,
+ *   scales[r] = (max|v| / 127) * scale_mul.
+ * group_counts (may be NULL): row r is skipped (q and scales untouched) when
+ * group_counts[r / group_rows] == 0.  K % 16 == 0 (K % 128 with the
+ * rotation), K <= 16384. */
+int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float scale_mul,
+                      int group_rows, const int32_t* group_counts, int8_t* q, float* scales,
+                      void* stream);
+
+/* int8 grouped GEMM: groups as moe_grouped_gemm; a [M, K] and w [G, N, K]
+ * int8, int32 accumulation (exact), then
+ *   out[r, n] = bf16(float(acc) * (sa(r) * w_scales[g, n]))
+ * with sa(r) = a_scales[a_scale_idx ? a_scale_idx[r] : r], or
+ * ident_scales[i] for row i of an identity group (which reads ident_a).
+ * K % 128 == 0. */
+int moe_grouped_gemm_i8(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+                        const int8_t* w, const float* w_scales, const int32_t* offs, int G, int M,
+                        int N, int K, const int8_t* ident_a, const float* ident_scales,
+                        int ident_m, void* out, void* ws, size_t ws_bytes, void* stream);
+
+/* int8 SwiGLU grouped GEMM: h[r, n] = bf16(silu(g) * u) with g and u the
+ * dequantised int8 products of a with wg[g] and wu[g] (scales as above). */
+int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+                          const int8_t* wg, const float* wg_scales, const int8_t* wu,
+                          const float* wu_scales, const int32_t* offs, int G, int M, int N, int K,
+                          const int8_t* ident_a, const float* ident_scales, int ident_m, void* h,
+                          void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,6 +23,13 @@ configurations name:
 * expert grouped GEMM     moe_gemm.h:66-95, moe_gemm.cu:616-650 (grouped_mm /
                           grouped_mm_pair over inclusive group ends offs; the
                           SwiGLU h = silu(g) * u of the expert MLP)
+* int8 experts            per-row int8 quantisation with an optional block
+                          Walsh-Hadamard rotation (the reference's xquant /
+                          hquant / wquant, kernel.cu:61-66, kernel.cu:125-129,
+                          moe_wq.h:150-188, here with per-row scales and
+                          128-blocks) and the int8 grouped GEMMs
+                          (moe_int8.h:27-45): exact integer products, then
+                          float(acc) * (row scale * column scale)
 
 Two deliberate differences from the reference, shared by the HIP kernels:
 
@@ -383,6 +390,78 @@ def grouped_swiglu(a, wg, wu, offs_incl, ident_a=None, ident_m=0):
     g = grouped_gemm(a, wg, offs_incl, ident_a, ident_m)
     u = grouped_gemm(a, wu, offs_incl, ident_a, ident_m)
     return silu(g) * u
+
+
+# ---------------------------------------------------------------------------
+# int8 experts
+# ---------------------------------------------------------------------------
+def fwht_blocks(v, n=128):
+    """Unnormalised Walsh-Hadamard transform of each n-block of the last
+    axis, in fp32, butterfly stages s = 1, 2, ..., n/2 (for k with bit s
+    clear: v[k] = a + b, v[k^s] = a - b, a = v[k], b = v[k^s]) -- the order
+    of moe_wq.h:178-188's wht16, over 128 points."""
+    v = np.asarray(v, dtype=f32).copy()
+    sh = v.shape
+    s = 1
+    while s < n:
+        b = v.reshape(-1, n // (2 * s), 2, s)
+        lo = b[:, :, 0, :].copy()
+        hi = b[:, :, 1, :].copy()
+        b[:, :, 0, :] = lo + hi
+        b[:, :, 1, :] = lo - hi
+        s *= 2
+    return v.reshape(sh)
+
+
+def quant_rows_i8(x, hadamard=0, scale_mul=1.0):
+    """Per-row symmetric int8 of bf16 rows x [R, K] (optionally rotated):
+    q = clamp(rint(v * (127 / amax)), -127, 127), s = (amax / 127) * scale_mul,
+    all in fp32 (rint = round half to even); an all-zero row gives q = 0, s = 0.
+    Returns (q int8 [R, K], s fp32 [R])."""
+    v = torch.as_tensor(x).float().numpy().astype(f32)
+    if hadamard:
+        v = fwht_blocks(v, hadamard)
+    amax = np.abs(v).max(axis=1).astype(f32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(amax > 0, f32(127.0) / amax, f32(0.0)).astype(f32)
+    q = np.clip(np.rint(v * inv[:, None]), -127, 127).astype(np.int8)
+    s = ((amax / f32(127.0)).astype(f32) * f32(scale_mul)).astype(f32)
+    return q, s
+
+
+def grouped_gemm_i8(a, a_scales, w, w_scales, offs_incl, a_scale_idx=None, ident_a=None,
+                    ident_scales=None, ident_m=0):
+    """out[r, n] = float32(sum_k a[r,k] w[g,n,k]) * (sa(r) * w_scales[g, n]),
+    fp32 (bf16 rounding is the caller's).  The integer sums are formed in
+    float64, which is exact (|sum| <= 127^2 K < 2^53).  sa(r) =
+    a_scales[a_scale_idx[r]] (or a_scales[r]); an identity group reads ident_a
+    and ident_scales.  Rows outside every group stay 0."""
+    a = np.asarray(a, dtype=np.int8)
+    w = np.asarray(w, dtype=np.int8)
+    ws = np.asarray(w_scales, dtype=f32)
+    M = a.shape[0]
+    rs = np.asarray(a_scales, dtype=f32)
+    if a_scale_idx is not None:
+        rs = rs[np.asarray(a_scale_idx, dtype=np.int64)]
+    out = np.zeros((M, w.shape[1]), dtype=f32)
+    for g, (lo, hi) in enumerate(group_bounds(offs_incl, M)):
+        if hi <= lo:
+            continue
+        if ident_m and hi - lo == ident_m:
+            ag = np.asarray(ident_a, dtype=np.int8)[:ident_m]
+            sg = np.asarray(ident_scales, dtype=f32)[:ident_m]
+        else:
+            ag, sg = a[lo:hi], rs[lo:hi]
+        acc = (ag.astype(np.float64) @ w[g].astype(np.float64).T).astype(f32)
+        out[lo:hi] = acc * (sg[:, None] * ws[g][None, :]).astype(f32)
+    return out
+
+
+def grouped_swiglu_i8(a, a_scales, wg, wg_scales, wu, wu_scales, offs_incl, **kw):
+    """h = silu(g) * u of the two dequantised int8 products (fp32)."""
+    g = grouped_gemm_i8(a, a_scales, wg, wg_scales, offs_incl, **kw)
+    u = grouped_gemm_i8(a, a_scales, wu, wu_scales, offs_incl, **kw)
+    return silu(g) * torch.as_tensor(u)
 
 
 # ---------------------------------------------------------------------------

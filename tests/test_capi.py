@@ -148,6 +148,37 @@ def test_grouped_gemm_validation():
     assert L.moe_grouped_gemm_workspace_bytes(-1) == 0
 
 
+def test_int8_validation():
+    L = M.lib()
+    ws = ctypes.c_void_p(0x10000)
+    # a, a_scales, a_scale_idx, w, w_scales, offs, G, M, N, K, ident_a, ident_scales, ident_m,
+    # out, ws, ws_bytes, stream
+    args = lambda G=4, Mr=64, K=256, sc=FAKE, ia=None, isc=None, im=0, idx=None, wsb=4096: (
+        FAKE, sc, idx, FAKE, FAKE, FAKE, G, Mr, 128, K, ia, isc, im, FAKE, ws, wsb, None)
+    err(L.moe_grouped_gemm_i8(*args(K=192)), -3, "multiple of 128")
+    err(L.moe_grouped_gemm_i8(*args(G=0)), -2, "G=0")
+    err(L.moe_grouped_gemm_i8(*args(sc=None)), -1, "scales")
+    err(L.moe_grouped_gemm_i8(*args(im=8, ia=FAKE)), -1, "ident_scales")
+    err(L.moe_grouped_gemm_i8(*args(idx=ctypes.c_void_p(0x10002))), -6)
+    err(L.moe_grouped_gemm_i8(*args(wsb=8)), -4, "workspace")
+    err(L.moe_grouped_swiglu_i8(FAKE, FAKE, None, FAKE, FAKE, FAKE, None, FAKE, 4, 64, 128, 256,
+                                None, None, 0, FAKE, ws, 4096, None), -1)
+    # x, R, K, hadamard, scale_mul, group_rows, group_counts, q, scales, stream
+    q = lambda R=4, K=256, had=0, mul=1.0, gr=0, gc=None, x=FAKE: (
+        x, R, K, had, mul, gr, gc, FAKE, FAKE, None)
+    err(L.moe_quant_rows_i8(*q(had=64)), -2, "hadamard")
+    err(L.moe_quant_rows_i8(*q(K=200, had=128)), -3, "multiple of 128")
+    err(L.moe_quant_rows_i8(*q(K=24)), -3, "multiple of 16")
+    err(L.moe_quant_rows_i8(*q(K=16384 + 128)), -3)
+    err(L.moe_quant_rows_i8(*q(mul=0.0)), -2, "scale_mul")
+    err(L.moe_quant_rows_i8(*q(mul=float("inf"))), -2, "scale_mul")
+    err(L.moe_quant_rows_i8(*q(gc=FAKE)), -2, "group_rows")
+    err(L.moe_quant_rows_i8(*q(x=None)), -1)
+    err(L.moe_quant_rows_i8(*q(x=ctypes.c_void_p(0x10008))), -6)
+    err(L.moe_quant_rows_i8(*q(R=-1)), -2)
+    assert L.moe_quant_rows_i8(*q(R=0, x=None)) == 0   # nothing to do: no pointer needed
+
+
 def test_python_layer_refuses_cpu_tensors():
     x = torch.zeros(4, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="no CPU path"):

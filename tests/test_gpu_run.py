@@ -59,17 +59,21 @@ def test_run_matches_reference_semantics(cuda):
     assert float((err <= 0.02 + 0.05 * acc.abs()).float().mean()) >= 0.99   # the harness gate, K:1640-1642
 
 
-@pytest.mark.parametrize("S,atol,dispatch,need", [
-    (1571, 0.010, "bf16", 0.99),
-    (4096, 0.014, "bf16", 0.99),
-    (8192, 0.012, "bf16", 0.99),
+@pytest.mark.parametrize("S,atol,dispatch,need,experts", [
+    (1571, 0.010, "bf16", 0.99, "bf16"),
+    (4096, 0.014, "bf16", 0.99, "bf16"),
+    (8192, 0.012, "bf16", 0.99, "bf16"),
+    # int8 experts, the reference's own precision choice (kernel.cu:61-66)
+    (1571, 0.010, "bf16", 0.99, "int8"),
+    (4096, 0.014, "bf16", 0.99, "int8"),
+    (8192, 0.012, "bf16", 0.99, "int8"),
     # fp8 dispatch (e4m3fn rows, per-128 scales) is a precision trade-off the
     # reference's gate does not admit at T = 1571: 97.9% of elements inside
     # atol + 5% (measured on MI355X) against the 99% required.  The case pins
     # that measured fraction; bf16 dispatch is the drop-in.
-    (1571, 0.010, "fp8", 0.975),
+    (1571, 0.010, "fp8", 0.975, "bf16"),
 ])
-def test_run_at_reference_workload_shape(cuda, S, atol, dispatch, need):
+def test_run_at_reference_workload_shape(cuda, S, atol, dispatch, need, experts):
     """run() at the reference's own workload shapes: T in {1571, 4096, 8192}
     (B=1), H = 8192, NE = 64, Ni = 3584, shared SNi = 7168 (K:133-136,
     K:4081-4126), with the harness's input distribution (K:1292-1297) and its
@@ -89,7 +93,9 @@ def test_run_at_reference_workload_shape(cuda, S, atol, dispatch, need):
     sg = (r(SNi, H) / H ** 0.5).to(torch.bfloat16)
     su = (r(SNi, H) / H ** 0.5).to(torch.bfloat16)
     sd = (r(H, SNi) / SNi ** 0.5).to(torch.bfloat16)
-    out, logits = M.run(hs, gw, bias, eg, eu, ed, sg, su, sd, 1e-20, dispatch=dispatch)
+    print("run T=%d dispatch=%s experts=%s" % (B * S, dispatch, experts), flush=True)
+    out, logits = M.run(hs, gw, bias, eg, eu, ed, sg, su, sd, 1e-20, dispatch=dispatch,
+                        experts=experts)
     torch.cuda.synchronize()
     T = B * S
     x = hs.view(T, H).float()
@@ -108,7 +114,8 @@ def test_run_at_reference_workload_shape(cuda, S, atol, dispatch, need):
         ref.index_add_(0, tok, w_t[tok, slot][:, None] * (h @ ed[e].float().t()))
     ok = (out.view(T, H).float() - ref).abs() <= atol + 0.05 * ref.abs()
     frac = float(ok.float().mean())
-    print("T=%d dispatch=%s: %.5f of elements inside the gate" % (T, dispatch, frac))
+    print("T=%d dispatch=%s experts=%s: %.5f of elements inside the gate"
+          % (T, dispatch, experts, frac))
     assert frac >= need, frac
 
 
@@ -142,3 +149,32 @@ def test_run_fp8_dispatch_small_shape(cuda):
     assert float((err <= 0.02 + 0.05 * acc.abs()).float().mean()) >= 0.99   # K:1640-1642
     d = (out8.float() - out16.float()).abs()
     assert float(d.max()) <= 0.1 * float(out16.float().abs().max())
+
+
+def test_run_int8_experts_small_shape(cuda):
+    """run(..., experts="int8") at a small shape with tokens spread over many
+    experts (not the harness's 8 hot experts): against the CPU fp32 evaluation
+    with the harness gate form at atol 0.02, and close to the bf16 path."""
+    args = make(seed=5)
+    norm_min = 1e-6
+    dev_args = [a.to(cuda) for a in args]
+    out8, logits8 = M.run(*dev_args, norm_min, experts="int8")
+    out16, logits16 = M.run(*dev_args, norm_min)
+    torch.cuda.synchronize()
+    assert torch.equal(logits8, logits16)
+    hs, gw, bias, eg, eu, ed, sg, su, sd = args
+    B, S, H = hs.shape
+    T = B * S
+    ids, wts = O.score_topk(logits8.cpu().numpy(), bias.numpy(), 8,
+                            O.RouteCfg(O.SCORING_SOFTMAX_BIAS, norm_min=norm_min))
+    xf = hs.view(T, H).float()
+    acc = (torch.nn.functional.silu(xf @ sg.float().t()) * (xf @ su.float().t())) @ sd.float().t()
+    for t in range(T):
+        for j in range(8):
+            e = int(ids[t, j])
+            h = torch.nn.functional.silu(xf[t] @ eg[e].float().t()) * (xf[t] @ eu[e].float().t())
+            acc[t] += float(wts[t, j]) * (h @ ed[e].float().t())
+    err = (out8.view(T, H).float().cpu() - acc).abs()
+    assert float((err <= 0.02 + 0.05 * acc.abs()).float().mean()) >= 0.99   # K:1640-1642
+    with pytest.raises(RuntimeError):
+        M.run(*dev_args, norm_min, experts="int8", dispatch="fp8")

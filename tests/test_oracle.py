@@ -22,6 +22,11 @@ function is pinned here by something other than its own formula:
 |                       | return a; identity shortcut reads ident_a                         |
 | grouped_swiglu        | float64 math.exp closed form x / (1 + e^-x) * u                   |
 | dequant_fp8_rows      | hand e4m3fn decoder x scale in numpy fp32, hand bf16 nearest-even |
+| fwht_blocks           | scipy.linalg.hadamard (Sylvester) matrix product; H H = 128 I     |
+| quant_rows_i8         | hand rows (half-even ties, zero row, clamp); error <= s/2;        |
+|                       | rotated pair / 128 contracts to the unrotated product             |
+| grouped_gemm_i8       | brute-force Python integer loop; scale index / identity groups;  |
+|                       | dequantised float64 product                                      |
 """
 import itertools
 import math
@@ -395,3 +400,81 @@ def test_dequant_fp8_rows_hand_decoder():
     for c in keep:
         prod = np.float32(e4m3fn_decode(c)) * np.float32(1.0 / 3.0)
         assert got2[c] == _bf16_rne_bits(np.float32(prod)), c
+
+
+# ---------------------------------------------------------------------------
+# int8 experts
+# ---------------------------------------------------------------------------
+def test_fwht_blocks_is_sylvester_hadamard():
+    from scipy.linalg import hadamard
+    rng = np.random.default_rng(11)
+    v = rng.integers(-50, 50, size=(3, 256)).astype(f32)   # integer sums: exact in fp32
+    Hm = hadamard(128).astype(np.float64)
+    ref = np.concatenate([v[:, :128] @ Hm, v[:, 128:] @ Hm], axis=1)
+    assert np.array_equal(O.fwht_blocks(v), ref.astype(f32))
+    # involution up to the factor n: H H = 128 I
+    assert np.array_equal(O.fwht_blocks(O.fwht_blocks(v)), (128 * v).astype(f32))
+
+
+def test_quant_rows_i8_hand_rows():
+    # amax = 127 -> 127 / amax = 1: q = rint(v), ties to even
+    row = np.zeros(16, dtype=f32)
+    row[:8] = [127, 2.5, 3.5, -0.5, -1.5, 0.25, -127, 126.5]
+    x = torch.tensor(np.stack([row, np.zeros(16, f32), row * 2]), dtype=torch.bfloat16)
+    q, s = O.quant_rows_i8(x, scale_mul=0.5)
+    assert q[0, :8].tolist() == [127, 2, 4, 0, -2, 0, -127, 126]
+    assert q[1].tolist() == [0] * 16 and s[1] == 0.0
+    assert s[0] == f32(0.5) and s[2] == f32(1.0)   # (amax / 127) * scale_mul
+    assert q[2, :8].tolist() == [127, 2, 4, 0, -2, 0, -127, 126]
+
+
+def test_quant_rows_i8_error_bound_and_rotation_fold():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(6, 512, generator=g).to(torch.bfloat16)
+    w = torch.randn(5, 512, generator=g).to(torch.bfloat16)
+    q, s = O.quant_rows_i8(x)
+    xf = x.double().numpy()
+    assert np.all(np.abs(q * s[:, None].astype(np.float64) - xf) <= s[:, None] / 2 * (1 + 1e-6))
+    assert np.abs(q).max() == 127
+    # rotated on both sides, 1/128 folded into one scale: the same product
+    qx, sx = O.quant_rows_i8(x, hadamard=128)
+    qw, sw = O.quant_rows_i8(w, hadamard=128, scale_mul=1 / 128)
+    got = (qx.astype(np.float64) @ qw.astype(np.float64).T) * sx[:, None] * sw[None, :]
+    ref = xf @ w.double().numpy().T
+    assert np.abs(got - ref).max() <= 0.02 * np.abs(ref).max()
+    # the rotated operand is quantised to within half a step of the Hadamard
+    # transform of its rows
+    rot = O.fwht_blocks(x.float().numpy())
+    assert np.all(np.abs(qx * sx[:, None].astype(np.float64) - rot) <= sx[:, None] / 2 * (1 + 1e-6))
+
+
+def test_grouped_gemm_i8_brute_force():
+    rng = np.random.default_rng(5)
+    M, N, K, G = 11, 5, 8, 3
+    a = rng.integers(-127, 128, size=(M, K)).astype(np.int8)
+    w = rng.integers(-127, 128, size=(G, N, K)).astype(np.int8)
+    rs = rng.random(7).astype(f32) + f32(0.5)
+    idx = rng.integers(0, 7, size=M).astype(np.int32)
+    ws = rng.random((G, N)).astype(f32)
+    ident = rng.integers(-127, 128, size=(4, K)).astype(np.int8)
+    ids = rng.random(4).astype(f32)
+    offs = [3, 7, 9]                     # groups of 3, 4 (identity), 2 rows; rows 9-10 outside
+    got = O.grouped_gemm_i8(a, rs, w, ws, offs, a_scale_idx=idx, ident_a=ident,
+                            ident_scales=ids, ident_m=4)
+    bounds = [(0, 3), (3, 7), (7, 9)]
+    for r in range(M):
+        for n in range(N):
+            gg = [g for g, (lo, hi) in enumerate(bounds) if lo <= r < hi]
+            if not gg:
+                assert got[r, n] == 0
+                continue
+            g = gg[0]
+            if g == 1:
+                arow, sa = ident[r - 3], ids[r - 3]
+            else:
+                arow, sa = a[r], rs[idx[r]]
+            acc = sum(int(arow[k]) * int(w[g, n, k]) for k in range(K))
+            assert got[r, n] == f32(acc) * (sa * ws[g, n])
+    # against the dequantised float64 product
+    deq = (a.astype(np.float64) * rs[idx][:, None]) @ (w[0].astype(np.float64) * ws[0][:, None]).T
+    assert np.allclose(got[:3], deq[:3], rtol=1e-6, atol=1e-6)
