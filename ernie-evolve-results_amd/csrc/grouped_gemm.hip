@@ -420,9 +420,11 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   }
 
   // Epilogue: lane holds rows (lane>>4)*4 + r, column lane & 15 of each 16x16 tile.
-  // int8: value = float(acc) * (row scale * column scale), in that order.
-  const int ldo = N;
-  float cs0[FN], cs1[FN];  // int8 column scales of this lane's columns
+  // int8: value = float(acc) * (row scale * column scale), in that order.  All
+  // scales are loaded before the first store (a load issued after a store
+  // would wait for it: both count in vmcnt).
+  constexpr int OUTC = SWIGLU ? BN / 2 : BN;  // output columns of a tile
+  float cs0[FN], cs1[FN], rsc[FM][4];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     cs0[j] = cs1[j] = 1.0f;
@@ -439,35 +441,76 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
+      rsc[i][r] = 1.0f;
+      if constexpr (I8) {
+        const int row = min(r0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r, rlast);
+        rsc[i][r] = ident ? i8s.ident[row - gs] : i8s.a[i8s.a_idx ? i8s.a_idx[row] : row];
+      }
+    }
+  // output value of accumulator (i, j, r); SwiGLU pairs j (gate) with j + 1 (up)
+  auto value = [&](int i, int j, int r) -> float {
+    if (SWIGLU) {
+      float gv, uv;
+      if constexpr (I8) {
+        gv = (float)acc[i][j][r] * (rsc[i][r] * cs0[j]);
+        uv = (float)acc[i][j + 1][r] * (rsc[i][r] * cs1[j]);
+      } else {
+        gv = acc[i][j][r];
+        uv = acc[i][j + 1][r];
+      }
+      return swiglu(gv, uv);
+    }
+    if constexpr (I8) return (float)acc[i][j][r] * (rsc[i][r] * cs0[j]);
+    else return acc[i][j][r];
+  };
+  constexpr int JSTEP = SWIGLU ? 2 : 1;
+  const int ldo = N;
+  if ((N & 7) == 0) {
+    // Stage the bf16 tile in LDS (the operand buffers are idle once every wave is
+    // past its last fragment read), then write whole 16-byte chunks of output
+    // rows.  LDS row = OUTC bf16; 16-byte chunk c of tile row rl sits at
+    // c ^ (2 * ((rl >> 2) & 3)), so the four row groups one ds_write covers
+    // land in distinct banks.
+    static_assert(BM * OUTC * 2 <= (int)sizeof(lds), "output tile fits in the LDS");
+    constexpr int RCH = OUTC / 8;
+    unsigned short* ct = reinterpret_cast<unsigned short*>(lds);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int rl = wm * WTM + i * 16 + (lane >> 4) * 4 + r;
+        const int sw = 2 * ((rl >> 2) & 3);
+#pragma unroll
+        for (int j = 0; j < FN; j += JSTEP) {
+          const int cl = (SWIGLU ? (wn * FN + j) / 2 * 16 : wn * WTN + j * 16) + (lane & 15);
+          ct[rl * OUTC + (((cl >> 3) ^ sw) << 3) + (cl & 7)] = (unsigned short)f2bf(value(i, j, r));
+        }
+      }
+    __syncthreads();
+    const int c0 = nt * OUTC;
+    for (int q = threadIdx.x; q < BM * RCH; q += NT) {
+      const int rl = q / RCH, c = q % RCH;
+      const int row = r0 + rl, col = c0 + c * 8;
+      if (row > rlast || col >= N) continue;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(ct + rl * OUTC +
+                                                      ((c ^ (2 * ((rl >> 2) & 3))) << 3));
+      *reinterpret_cast<u32x4*>(out + (long long)row * ldo + col) = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
       const int row = r0 + wm * WTM + i * 16 + (lane >> 4) * 4 + r;
       if (row > rlast) continue;
-      float rs = 1.0f;
-      if constexpr (I8)
-        rs = ident ? i8s.ident[row - gs] : i8s.a[i8s.a_idx ? i8s.a_idx[row] : row];
       unsigned short* orow = out + (long long)row * ldo;
-      if (SWIGLU) {
 #pragma unroll
-        for (int j = 0; j < FN; j += 2) {
-          const int col = nt * (BN / 2) + (wn * FN + j) / 2 * 16 + (lane & 15);
-          float gv, uv;
-          if constexpr (I8) {
-            gv = (float)acc[i][j][r] * (rs * cs0[j]);
-            uv = (float)acc[i][j + 1][r] * (rs * cs1[j]);
-          } else {
-            gv = acc[i][j][r];
-            uv = acc[i][j + 1][r];
-          }
-          if (col < N) orow[col] = (unsigned short)f2bf(swiglu(gv, uv));
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = nt * BN + wn * WTN + j * 16 + (lane & 15);
-          float v;
-          if constexpr (I8) v = (float)acc[i][j][r] * (rs * cs0[j]);
-          else v = acc[i][j][r];
-          if (col < N) orow[col] = (unsigned short)f2bf(v);
-        }
+      for (int j = 0; j < FN; j += JSTEP) {
+        const int col = SWIGLU ? nt * (BN / 2) + (wn * FN + j) / 2 * 16 + (lane & 15)
+                               : nt * BN + wn * WTN + j * 16 + (lane & 15);
+        if (col < N) orow[col] = (unsigned short)f2bf(value(i, j, r));
       }
     }
 }
