@@ -400,10 +400,11 @@ int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float sca
                       void* stream) {
   if (R < 0 || K < 1) return fail(MOE_ERR_INVALID_ARG, "R=%lld, K=%d", R, K);
   if (R >= (1ll << 31)) return fail(MOE_ERR_UNSUPPORTED, "R=%lld rows exceeds the grid", R);
-  if (hadamard != 0 && hadamard != 128)
-    return fail(MOE_ERR_INVALID_ARG, "hadamard=%d (0 or 128)", hadamard);
-  if (K % (hadamard ? 128 : 16) != 0)
-    return fail(MOE_ERR_UNSUPPORTED, "K=%d is not a multiple of %d", K, hadamard ? 128 : 16);
+  if (hadamard != 0 && hadamard != 16 && hadamard != 128)
+    return fail(MOE_ERR_INVALID_ARG, "hadamard=%d (0, 16 or 128)", hadamard);
+  if (K % (hadamard == 128 ? 128 : 16) != 0)
+    return fail(MOE_ERR_UNSUPPORTED, "K=%d is not a multiple of %d", K,
+                hadamard == 128 ? 128 : 16);
   if (K > moe::quant_rows_max_k())
     return fail(MOE_ERR_UNSUPPORTED, "K=%d > %d", K, moe::quant_rows_max_k());
   if (!(scale_mul > 0.0f) || !std::isfinite(scale_mul))
@@ -415,7 +416,7 @@ int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float sca
   if ((x && !aligned16(x)) || (q && !aligned16(q)) || (scales && ((uintptr_t)scales & 3u)) ||
       (group_counts && ((uintptr_t)group_counts & 3u)))
     return fail(MOE_ERR_ALIGNMENT, "x and q must be 16-byte aligned, scales 4-byte aligned");
-  return launched(moe::launch_quant_rows_i8((const __bf16*)x, R, K, hadamard != 0, scale_mul,
+  return launched(moe::launch_quant_rows_i8((const __bf16*)x, R, K, hadamard, scale_mul,
                                             group_rows, group_counts, (signed char*)q, scales,
                                             (hipStream_t)stream),
                   "quant_rows_i8");

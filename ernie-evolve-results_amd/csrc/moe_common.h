@@ -74,9 +74,10 @@ hipError_t launch_grouped_gemm_i8(const void* a, const float* a_rs, const int32_
                                   const void* w0, const float* w0s, const void* w1,
                                   const float* w1s, const int32_t* offs, int G, int M, int N, int K,
                                   bool swiglu, void* out, int32_t* tile_start, hipStream_t s);
-// Per-row int8 quantisation, optional 128-block Walsh-Hadamard rotation.
+// Per-row int8 quantisation, optional 16- or 128-block Walsh-Hadamard rotation
+// (had = 0, 16, 128).
 int quant_rows_max_k();
-hipError_t launch_quant_rows_i8(const __bf16* x, long long R, int K, bool had, float scale_mul,
+hipError_t launch_quant_rows_i8(const __bf16* x, long long R, int K, int had, float scale_mul,
                                 int group_rows, const int* counts, signed char* q, float* s,
                                 hipStream_t st);
 

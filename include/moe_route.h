@@ -184,13 +184,14 @@ int moe_grouped_swiglu_fp8(const void* a, const float* a_scales, const void* wg,
  * moe_int8.h:27-45 / moe_int8.cu:391-393, the quantiser moe_wq.h:150-188).
  *
  * Per-row symmetric int8 quantisation of R rows of K bf16 values:
- *   v = the row (hadamard == 128: rotated in blocks of 128 along the row by the
- *       unnormalised Walsh-Hadamard transform, butterfly stages 1, 2, ..., 64),
+ *   v = the row (hadamard == 16 or 128: rotated in blocks of that size along
+ *       the row by the unnormalised Walsh-Hadamard transform, butterfly stages
+ *       1, 2, ..., hadamard / 2),
  *   q = clamp(rint(v * (127 / max|v|)), -127, 127), 0 for an all-zero row,
  *   scales[r] = (max|v| / 127) * scale_mul.
  * group_counts (may be NULL): row r is skipped (q and scales untouched) when
  * group_counts[r / group_rows] == 0.  K % 16 == 0 (K % 128 with the
- * rotation), K <= 16384. */
+ * 128-point rotation), K <= 16384. */
 int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float scale_mul,
                       int group_rows, const int32_t* group_counts, int8_t* q, float* scales,
                       void* stream);

@@ -27,7 +27,7 @@ configurations name:
                           Walsh-Hadamard rotation (the reference's xquant /
                           hquant / wquant, kernel.cu:61-66, kernel.cu:125-129,
                           moe_wq.h:150-188, here with per-row scales and
-                          128-blocks) and the int8 grouped GEMMs
+                          16- or 128-point blocks) and the int8 grouped GEMMs
                           (moe_int8.h:27-45): exact integer products, then
                           float(acc) * (row scale * column scale)
 

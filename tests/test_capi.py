@@ -169,6 +169,7 @@ def test_int8_validation():
     err(L.moe_quant_rows_i8(*q(had=64)), -2, "hadamard")
     err(L.moe_quant_rows_i8(*q(K=200, had=128)), -3, "multiple of 128")
     err(L.moe_quant_rows_i8(*q(K=24)), -3, "multiple of 16")
+    err(L.moe_quant_rows_i8(*q(K=40, had=16)), -3, "multiple of 16")
     err(L.moe_quant_rows_i8(*q(K=16384 + 128)), -3)
     err(L.moe_quant_rows_i8(*q(mul=0.0)), -2, "scale_mul")
     err(L.moe_quant_rows_i8(*q(mul=float("inf"))), -2, "scale_mul")

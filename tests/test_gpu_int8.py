@@ -28,6 +28,7 @@ def inclusive(sizes, dev):
 @pytest.mark.parametrize("R,K,had,mul", [
     (5, 16, 0, 1.0), (33, 3584, 0, 1.0), (33, 3584, 128, 1.0), (17, 8192, 0, 1.0),
     (17, 8192, 128, 1.0 / 128), (3, 16384, 128, 0.5), (9, 4224, 128, 1.0),
+    (33, 3584, 16, 1.0 / 16), (6, 8192, 16, 1.0), (5, 48, 16, 1.0), (7, 12304, 16, 1.0),
 ])
 def test_quant_rows_bit_exact(cuda, R, K, had, mul):
     g = torch.Generator().manual_seed(R * 7 + K)
@@ -143,8 +144,8 @@ def test_int8_chain_matches_float_product(cuda):
     x = torch.randn(T, H, generator=g, device=cuda).to(torch.bfloat16)
     wd = (torch.randn(1, H, Ni, generator=g, device=cuda) / Ni ** 0.5).to(torch.bfloat16)
     h = torch.randn(T, Ni, generator=g, device=cuda).to(torch.bfloat16)
-    hq, hs = M.quant_rows_i8(h, hadamard=128)
-    wq, wsc = M.quant_rows_i8(wd, hadamard=128, scale_mul=1 / 128)
+    hq, hs = M.quant_rows_i8(h, hadamard=16)
+    wq, wsc = M.quant_rows_i8(wd, hadamard=16, scale_mul=1 / 16)
     ends = torch.tensor([T], dtype=torch.int32, device=cuda)
     y = M.grouped_gemm_i8(hq, hs, wq, wsc, ends).float()
     ref = h.float() @ wd[0].float().t()

@@ -414,6 +414,9 @@ def test_fwht_blocks_is_sylvester_hadamard():
     assert np.array_equal(O.fwht_blocks(v), ref.astype(f32))
     # involution up to the factor n: H H = 128 I
     assert np.array_equal(O.fwht_blocks(O.fwht_blocks(v)), (128 * v).astype(f32))
+    H16 = hadamard(16).astype(np.float64)
+    ref16 = (v.reshape(3, 16, 16).astype(np.float64) @ H16).reshape(3, 256)
+    assert np.array_equal(O.fwht_blocks(v, 16), ref16.astype(f32))
 
 
 def test_quant_rows_i8_hand_rows():
@@ -437,11 +440,13 @@ def test_quant_rows_i8_error_bound_and_rotation_fold():
     assert np.all(np.abs(q * s[:, None].astype(np.float64) - xf) <= s[:, None] / 2 * (1 + 1e-6))
     assert np.abs(q).max() == 127
     # rotated on both sides, 1/128 folded into one scale: the same product
-    qx, sx = O.quant_rows_i8(x, hadamard=128)
-    qw, sw = O.quant_rows_i8(w, hadamard=128, scale_mul=1 / 128)
-    got = (qx.astype(np.float64) @ qw.astype(np.float64).T) * sx[:, None] * sw[None, :]
     ref = xf @ w.double().numpy().T
-    assert np.abs(got - ref).max() <= 0.02 * np.abs(ref).max()
+    for n in (16, 128):
+        qx, sx = O.quant_rows_i8(x, hadamard=n)
+        qw, sw = O.quant_rows_i8(w, hadamard=n, scale_mul=1 / n)
+        got = (qx.astype(np.float64) @ qw.astype(np.float64).T) * sx[:, None] * sw[None, :]
+        assert np.abs(got - ref).max() <= 0.02 * np.abs(ref).max()
+    qx, sx = O.quant_rows_i8(x, hadamard=128)
     # the rotated operand is quantised to within half a step of the Hadamard
     # transform of its rows
     rot = O.fwht_blocks(x.float().numpy())
