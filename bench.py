@@ -267,7 +267,7 @@ def main():
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 experts, bf16 shared expert" if experts == "int8" else "bf16",
+        "dtype": "bf16",
         "data": "synthetic (seeded randn inputs generated on the GPU)",
         "config": {"workload": "%s route+dispatch+combine: %s" % (c.name, c.description),
                    "T": c.T, "H": c.H, "E": c.E, "k": c.k, "fp8_dispatch": c.fp8},
