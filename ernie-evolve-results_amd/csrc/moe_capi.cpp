@@ -409,8 +409,12 @@ int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float sca
     return fail(MOE_ERR_UNSUPPORTED, "K=%d > %d", K, moe::quant_rows_max_k());
   if (!(scale_mul > 0.0f) || !std::isfinite(scale_mul))
     return fail(MOE_ERR_INVALID_ARG, "scale_mul must be finite and > 0");
-  if (group_counts && group_rows < 1)
-    return fail(MOE_ERR_INVALID_ARG, "group_rows=%d with group_counts", group_rows);
+  if (group_counts && (group_rows < 1 || R % group_rows != 0))
+    return fail(MOE_ERR_INVALID_ARG, "group_rows=%d must divide R=%lld with group_counts",
+                group_rows, R);
+  if (group_counts && R / group_rows > moe::quant_rows_max_groups())
+    return fail(MOE_ERR_UNSUPPORTED, "%lld groups > %d", R / group_rows,
+                moe::quant_rows_max_groups());
   if (R > 0 && (!x || !q || !scales))
     return fail(MOE_ERR_NULL_POINTER, "x, q and scales are required");
   if ((x && !aligned16(x)) || (q && !aligned16(q)) || (scales && ((uintptr_t)scales & 3u)) ||

@@ -77,6 +77,7 @@ hipError_t launch_grouped_gemm_i8(const void* a, const float* a_rs, const int32_
 // Per-row int8 quantisation, optional 16- or 128-block Walsh-Hadamard rotation
 // (had = 0, 16, 128).
 int quant_rows_max_k();
+int quant_rows_max_groups();
 hipError_t launch_quant_rows_i8(const __bf16* x, long long R, int K, int had, float scale_mul,
                                 int group_rows, const int* counts, signed char* q, float* s,
                                 hipStream_t st);

@@ -22,8 +22,8 @@
 // group_counts[r / group_rows] == 0 (the weights of experts that received no
 // rows are never read).
 //
-// Layout: 256-thread blocks (at most 8 per CU, so rows of skipped groups cost
-// a branch, not a dispatched block), each taking RB consecutive rows per pass
+// Layout: 256-thread blocks (at most 8 per CU), which walk the rows of the
+// non-empty groups only (listed per block in LDS), RB consecutive rows per pass
 // (RB = 4 / 2 / 1 for K up to 4096 / 8192 / 16384) and issuing all their
 // loads before the first reduction; for one row, thread t holds 16 consecutive
 // elements of each 4096-wide chunk (two 16-byte loads).  A 16-point block is
@@ -37,6 +37,7 @@ namespace moe {
 constexpr int kQuantThreads = 256;
 constexpr int kQuantChunk = kQuantThreads * 16;  // elements per chunk
 constexpr int kQuantBlocks = 256 * 8;            // 8 resident blocks per CU
+constexpr int kQuantMaxGroups = 4096;            // groups gated by group_counts
 
 // v of lane (lane ^ m), m in {1, 2, 4}, through DPP moves (no LDS traffic):
 // quad permutations for 1 and 2, a row shift by 4 either way for 4.
@@ -57,17 +58,37 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_i8_kernel(
     const int* __restrict__ group_counts, signed char* __restrict__ q, float* __restrict__ s) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   __shared__ float part[RB][kQuantThreads / 64];
-  for (int rb = blockIdx.x * RB; rb < R; rb += gridDim.x * RB) {
-    // RB consecutive rows per pass: all their loads are issued together
+  // With group_counts, the rows to quantise are those of the non-empty groups:
+  // wave 0 lists them in LDS (ascending), and the blocks walk only those rows
+  // (virtual row v -> group grp[v / group_rows], row v % group_rows in it).
+  __shared__ int grp[kQuantMaxGroups];
+  __shared__ int n_grp;
+  int Rv = R;
+  if (group_counts) {
+    if (wave == 0) {
+      int n = 0;
+      const int G = R / group_rows;
+      for (int base = 0; base < G; base += 64) {
+        const bool live = base + lane < G && group_counts[base + lane] != 0;
+        const unsigned long long m = __ballot(live);
+        if (live) grp[n + __popcll(m & ((1ull << lane) - 1ull))] = base + lane;
+        n += __popcll(m);
+      }
+      if (lane == 0) n_grp = n;
+    }
+    __syncthreads();
+    Rv = n_grp * group_rows;
+  }
+  for (int rb = blockIdx.x * RB; rb < Rv; rb += gridDim.x * RB) {
+    // RB consecutive (virtual) rows per pass: all their loads are issued together
     bool act[RB];
-    bool any = false;
+    int rows[RB];
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
-      const int r = rb + i;
-      act[i] = r < R && !(group_counts && group_counts[r / group_rows] == 0);
-      any |= act[i];
+      const int v = rb + i;
+      act[i] = v < Rv;
+      rows[i] = group_counts ? grp[min(v, Rv - 1) / group_rows] * group_rows + v % group_rows : v;
     }
-    if (!any) continue;  // uniform over the block
     float v[RB][NC][16];
 #pragma unroll
     for (int i = 0; i < RB; ++i)
@@ -76,7 +97,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_i8_kernel(
         const int e0 = c * kQuantChunk + t * 16;
         u32x4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
         if (act[i] && e0 < K) {  // K % 16 == 0 (K % 128 == 0 with the 128-point rotation)
-          const __bf16* p = x + (long long)(rb + i) * K + e0;
+          const __bf16* p = x + (long long)rows[i] * K + e0;
           lo = ld_nt(reinterpret_cast<const u32x4*>(p));
           hi = ld_nt(reinterpret_cast<const u32x4*>(p + 8));
         }
@@ -129,7 +150,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_i8_kernel(
 #pragma unroll
     for (int i = 0; i < RB; ++i) {
       if (!act[i]) continue;
-      const int r = rb + i;
+      const int r = rows[i];
       const float am = fmaxf(fmaxf(part[i][0], part[i][1]), fmaxf(part[i][2], part[i][3]));
       const float inv = am > 0.0f ? 127.0f / am : 0.0f;
       if (t == 0) s[r] = (am / 127.0f) * scale_mul;
@@ -174,6 +195,7 @@ static void launch_nc(const __bf16* x, long long R, int K, int had, float scale_
 }
 
 int quant_rows_max_k() { return 4 * kQuantChunk; }
+int quant_rows_max_groups() { return kQuantMaxGroups; }
 
 hipError_t launch_quant_rows_i8(const __bf16* x, long long R, int K, int had, float scale_mul,
                                 int group_rows, const int* counts, signed char* q, float* s,

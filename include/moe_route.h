@@ -190,7 +190,8 @@ int moe_grouped_swiglu_fp8(const void* a, const float* a_scales, const void* wg,
  *   q = clamp(rint(v * (127 / max|v|)), -127, 127), 0 for an all-zero row,
  *   scales[r] = (max|v| / 127) * scale_mul.
  * group_counts (may be NULL): row r is skipped (q and scales untouched) when
- * group_counts[r / group_rows] == 0.  K % 16 == 0 (K % 128 with the
+ * group_counts[r / group_rows] == 0; group_rows must divide R, at most 4096
+ * groups.  K % 16 == 0 (K % 128 with the
  * 128-point rotation), K <= 16384. */
 int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float scale_mul,
                       int group_rows, const int32_t* group_counts, int8_t* q, float* scales,

@@ -174,6 +174,8 @@ def test_int8_validation():
     err(L.moe_quant_rows_i8(*q(mul=0.0)), -2, "scale_mul")
     err(L.moe_quant_rows_i8(*q(mul=float("inf"))), -2, "scale_mul")
     err(L.moe_quant_rows_i8(*q(gc=FAKE)), -2, "group_rows")
+    err(L.moe_quant_rows_i8(*q(R=6, gr=4, gc=FAKE)), -2, "divide")
+    err(L.moe_quant_rows_i8(*q(R=5000, gr=1, gc=FAKE)), -3, "groups")
     err(L.moe_quant_rows_i8(*q(x=None)), -1)
     err(L.moe_quant_rows_i8(*q(x=ctypes.c_void_p(0x10008))), -6)
     err(L.moe_quant_rows_i8(*q(R=-1)), -2)
