@@ -129,8 +129,8 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
 
 // Row / column scales of the int8 operands (unused by the bf16 and fp8 paths).
 struct I8Scales {
-  const float* a;      // [M] per row of a, or indexed through a_idx
-  const int* a_idx;    // NULL, or [M]: row r of a uses a[a_idx[r]]
+  const float* a;      // per row of a
+  const int* a_idx;    // NULL, or [M]: operand row r is row a_idx[r] of a (data and scale)
   const float* ident;  // [ident_m] per row of ident_a
   const float* w0;     // [G, N] per weight row of w0
   const float* w1;     // [G, N] per weight row of w1 (SwiGLU up)
@@ -230,8 +230,10 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     if (gi < A_INST) {
       const int r = gi * ARPI + lane / ACH, p = lane % ACH;
       const int row = min(r0 + r, rlast);  // rows past the group are loaded, never stored
+      int arow_i = row;
+      if constexpr (I8) arow_i = (!ident && i8s.a_idx) ? i8s.a_idx[row] : row;
       const char* arow = ident ? ident_a + (long long)(row - gs) * K * AEL
-                               : a + (long long)row * K * AEL;
+                               : a + (long long)arow_i * K * AEL;
       src[q] = arow + (p ^ swz(r, ACH)) * 16;
       kstep[q] = BK * AEL;
     } else {

@@ -341,7 +341,7 @@ int moe_grouped_swiglu_fp8(const void* a, const float* a_scales, const void* wg,
                         stream, true, true);
 }
 
-static int grouped_i8_common(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+static int grouped_i8_common(const int8_t* a, const float* a_scales, const int32_t* a_rows,
                              const int8_t* w0, const float* w0s, const int8_t* w1,
                              const float* w1s, const int32_t* offs, int G, int M, int N, int K,
                              const int8_t* ident_a, const float* ident_scales, int ident_m,
@@ -360,8 +360,8 @@ static int grouped_i8_common(const int8_t* a, const float* a_scales, const int32
     return fail(MOE_ERR_ALIGNMENT, "a, ident_a and the weights must be 16-byte aligned");
   if ((a_scales && ((uintptr_t)a_scales & 3u)) || (w0s && ((uintptr_t)w0s & 3u)) ||
       (w1s && ((uintptr_t)w1s & 3u)) || (ident_scales && ((uintptr_t)ident_scales & 3u)) ||
-      (a_scale_idx && ((uintptr_t)a_scale_idx & 3u)))
-    return fail(MOE_ERR_ALIGNMENT, "scales and a_scale_idx must be 4-byte aligned");
+      (a_rows && ((uintptr_t)a_rows & 3u)))
+    return fail(MOE_ERR_ALIGNMENT, "scales and a_rows must be 4-byte aligned");
   if ((long long)M * K >= (1ll << 40) || (long long)G * N * K >= (1ll << 40) ||
       (long long)G * N >= (1ll << 31))
     return fail(MOE_ERR_UNSUPPORTED, "operands too large");
@@ -372,26 +372,26 @@ static int grouped_i8_common(const int8_t* a, const float* a_scales, const int32
   const long long blocks = (((long long)M + 127) / 128 + G) *
                            moe::grouped_gemm_n_tiles(N, swiglu);
   if (blocks >= (1ll << 31)) return fail(MOE_ERR_UNSUPPORTED, "too many tiles (%lld)", blocks);
-  return launched(moe::launch_grouped_gemm_i8(a, a_scales, a_scale_idx, ident_a, ident_scales,
+  return launched(moe::launch_grouped_gemm_i8(a, a_scales, a_rows, ident_a, ident_scales,
                                               ident_m, w0, w0s, w1, w1s, offs, G, M, N, K, swiglu,
                                               out, (int32_t*)ws, (hipStream_t)stream),
                   swiglu ? "grouped_swiglu_i8" : "grouped_gemm_i8");
 }
 
-int moe_grouped_gemm_i8(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+int moe_grouped_gemm_i8(const int8_t* a, const float* a_scales, const int32_t* a_rows,
                         const int8_t* w, const float* w_scales, const int32_t* offs, int G, int M,
                         int N, int K, const int8_t* ident_a, const float* ident_scales,
                         int ident_m, void* out, void* ws, size_t ws_bytes, void* stream) {
-  return grouped_i8_common(a, a_scales, a_scale_idx, w, w_scales, w, w_scales, offs, G, M, N, K,
+  return grouped_i8_common(a, a_scales, a_rows, w, w_scales, w, w_scales, offs, G, M, N, K,
                            ident_a, ident_scales, ident_m, out, ws, ws_bytes, stream, false);
 }
 
-int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t* a_rows,
                           const int8_t* wg, const float* wg_scales, const int8_t* wu,
                           const float* wu_scales, const int32_t* offs, int G, int M, int N, int K,
                           const int8_t* ident_a, const float* ident_scales, int ident_m, void* h,
                           void* ws, size_t ws_bytes, void* stream) {
-  return grouped_i8_common(a, a_scales, a_scale_idx, wg, wg_scales, wu, wu_scales, offs, G, M, N,
+  return grouped_i8_common(a, a_scales, a_rows, wg, wg_scales, wu, wu_scales, offs, G, M, N,
                            K, ident_a, ident_scales, ident_m, h, ws, ws_bytes, stream, true);
 }
 

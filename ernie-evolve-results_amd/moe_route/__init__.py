@@ -356,9 +356,11 @@ def quant_rows_i8(x, hadamard=0, scale_mul=1.0, group_rows=0, group_counts=None,
     return q, scales
 
 
-def _i8_args(a, a_scales, offs, a_scale_idx, ident_a, ident_scales, ident_m):
+def _i8_args(a, a_scales, offs, a_rows, ident_a, ident_scales, ident_m):
     for t, n in ((a, "a"), (a_scales, "a_scales"), (offs, "offs")):
         _dev(t, n)
+    if a_rows is not None and (_dev(a_rows, "a_rows").dtype != torch.int32):
+        raise RuntimeError("a_rows must be int32")
     if a.dtype != torch.int8:
         raise RuntimeError("a must be int8")
     if offs.dtype != torch.int32:
@@ -369,36 +371,38 @@ def _i8_args(a, a_scales, offs, a_scale_idx, ident_a, ident_scales, ident_m):
                        dtype=torch.uint8, device=a.device)
 
 
-def grouped_gemm_i8(a, a_scales, w, w_scales, offs, a_scale_idx=None, ident_a=None,
+def grouped_gemm_i8(a, a_scales, w, w_scales, offs, a_rows=None, ident_a=None,
                     ident_scales=None, ident_m=0, out=None):
     """int8 grouped GEMM (the reference's int8 grouped_mm, moe_int8.h:27-45):
-    out[r, n] = bf16(float(a[r] . w[g, n]) * (sa(r) * w_scales[g, n])), exact
-    int32 accumulation; sa(r) = a_scales[a_scale_idx[r]] (or a_scales[r]).
-    a [M,K] int8, w [G,N,K] int8, w_scales [G,N] fp32; returns bf16 [M,N]."""
-    ws = _i8_args(a, a_scales, offs, a_scale_idx, ident_a, ident_scales, ident_m)
+    out[r, n] = bf16(float(A[r] . w[g, n]) * (sa(r) * w_scales[g, n])), exact
+    int32 accumulation, where operand row r is A[r] = a[a_rows[r]] with scale
+    sa(r) = a_scales[a_rows[r]] (a_rows None: a[r], a_scales[r]).  a int8
+    [rows, K], w [G,N,K] int8, w_scales [G,N] fp32; returns bf16 [M,N] with
+    M = len(a_rows) (or a's rows)."""
+    ws = _i8_args(a, a_scales, offs, a_rows, ident_a, ident_scales, ident_m)
     G, N, K = w.shape
-    M = a.shape[0]
+    M = a_rows.numel() if a_rows is not None else a.shape[0]
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
-    _check(lib().moe_grouped_gemm_i8(_ptr(a), _ptr(a_scales), _ptr(a_scale_idx), _ptr(w),
+    _check(lib().moe_grouped_gemm_i8(_ptr(a), _ptr(a_scales), _ptr(a_rows), _ptr(w),
                                      _ptr(w_scales), _ptr(offs), G, M, N, K, _ptr(ident_a),
                                      _ptr(ident_scales), int(ident_m), _ptr(out), _ptr(ws),
                                      ws.numel(), _stream(a)))
     return out
 
 
-def grouped_swiglu_i8(a, a_scales, wg, wg_scales, wu, wu_scales, offs, a_scale_idx=None,
+def grouped_swiglu_i8(a, a_scales, wg, wg_scales, wu, wu_scales, offs, a_rows=None,
                       ident_a=None, ident_scales=None, ident_m=0, out=None):
     """int8 SwiGLU grouped GEMM: h = bf16(silu(g) * u), g and u the dequantised
     int8 products of a with wg[g] and wu[g] (see grouped_gemm_i8)."""
-    ws = _i8_args(a, a_scales, offs, a_scale_idx, ident_a, ident_scales, ident_m)
+    ws = _i8_args(a, a_scales, offs, a_rows, ident_a, ident_scales, ident_m)
     if wg.shape != wu.shape:
         raise RuntimeError("gate and up weights must have one shape")
     G, N, K = wg.shape
-    M = a.shape[0]
+    M = a_rows.numel() if a_rows is not None else a.shape[0]
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
-    _check(lib().moe_grouped_swiglu_i8(_ptr(a), _ptr(a_scales), _ptr(a_scale_idx), _ptr(wg),
+    _check(lib().moe_grouped_swiglu_i8(_ptr(a), _ptr(a_scales), _ptr(a_rows), _ptr(wg),
                                        _ptr(wg_scales), _ptr(wu), _ptr(wu_scales), _ptr(offs), G,
                                        M, N, K, _ptr(ident_a), _ptr(ident_scales), int(ident_m),
                                        _ptr(out), _ptr(ws), ws.numel(), _stream(a)))
@@ -496,16 +500,15 @@ def _experts_int8(x, ids, E, wg, wu, wd):
     T, H = x.shape
     Ni = wg.shape[1]
     xq, xs = quant_rows_i8(x)
-    # the int8 rows travel through the row permute as 2-byte units
-    p = permute(xq.view(torch.bfloat16), ids, E)
-    xg = p["xg"].view(torch.int8)
+    # no gather: the expert GEMM reads token rows of xq through row_token
+    p = permute(x, ids, E, index_only=True)
     counts = p["counts"]
     ends = p["offsets"][1:]
     wgq, wgs = quant_rows_i8(wg, group_rows=Ni, group_counts=counts)
     wuq, wus = quant_rows_i8(wu, group_rows=Ni, group_counts=counts)
     wdq, wds = quant_rows_i8(wd, hadamard=INT8_HADAMARD, scale_mul=1.0 / INT8_HADAMARD,
                              group_rows=H, group_counts=counts)
-    h = grouped_swiglu_i8(xg, xs, wgq, wgs, wuq, wus, ends, a_scale_idx=p["row_token"],
+    h = grouped_swiglu_i8(xq, xs, wgq, wgs, wuq, wus, ends, a_rows=p["row_token"],
                           ident_a=xq, ident_scales=xs, ident_m=T)
     hq, hs = quant_rows_i8(h, hadamard=INT8_HADAMARD)
     return grouped_gemm_i8(hq, hs, wdq, wds, ends), p

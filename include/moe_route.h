@@ -197,20 +197,22 @@ int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float sca
                       int group_rows, const int32_t* group_counts, int8_t* q, float* scales,
                       void* stream);
 
-/* int8 grouped GEMM: groups as moe_grouped_gemm; a [M, K] and w [G, N, K]
- * int8, int32 accumulation (exact), then
- *   out[r, n] = bf16(float(acc) * (sa(r) * w_scales[g, n]))
- * with sa(r) = a_scales[a_scale_idx ? a_scale_idx[r] : r], or
- * ident_scales[i] for row i of an identity group (which reads ident_a).
+/* int8 grouped GEMM: groups as moe_grouped_gemm over M operand rows; w
+ * [G, N, K] int8; int32 accumulation (exact), then
+ *   out[r, n] = bf16(float(acc) * (sa(r) * w_scales[g, n])).
+ * Operand row r is row a_rows[r] of a (a_rows NULL: row r; a_rows lets the
+ * GEMM read token rows through moe_permute's row_token instead of a gather)
+ * and sa(r) its scale a_scales[a_rows[r]]; a row i of an identity group
+ * reads ident_a[i] and ident_scales[i].  a_rows values must be rows of a.
  * K % 128 == 0. */
-int moe_grouped_gemm_i8(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+int moe_grouped_gemm_i8(const int8_t* a, const float* a_scales, const int32_t* a_rows,
                         const int8_t* w, const float* w_scales, const int32_t* offs, int G, int M,
                         int N, int K, const int8_t* ident_a, const float* ident_scales,
                         int ident_m, void* out, void* ws, size_t ws_bytes, void* stream);
 
 /* int8 SwiGLU grouped GEMM: h[r, n] = bf16(silu(g) * u) with g and u the
  * dequantised int8 products of a with wg[g] and wu[g] (scales as above). */
-int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t* a_scale_idx,
+int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t* a_rows,
                           const int8_t* wg, const float* wg_scales, const int8_t* wu,
                           const float* wu_scales, const int32_t* offs, int G, int M, int N, int K,
                           const int8_t* ident_a, const float* ident_scales, int ident_m, void* h,

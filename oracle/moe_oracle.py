@@ -429,20 +429,22 @@ def quant_rows_i8(x, hadamard=0, scale_mul=1.0):
     return q, s
 
 
-def grouped_gemm_i8(a, a_scales, w, w_scales, offs_incl, a_scale_idx=None, ident_a=None,
+def grouped_gemm_i8(a, a_scales, w, w_scales, offs_incl, a_rows=None, ident_a=None,
                     ident_scales=None, ident_m=0):
-    """out[r, n] = float32(sum_k a[r,k] w[g,n,k]) * (sa(r) * w_scales[g, n]),
-    fp32 (bf16 rounding is the caller's).  The integer sums are formed in
-    float64, which is exact (|sum| <= 127^2 K < 2^53).  sa(r) =
-    a_scales[a_scale_idx[r]] (or a_scales[r]); an identity group reads ident_a
-    and ident_scales.  Rows outside every group stay 0."""
+    """out[r, n] = float32(sum_k A[r,k] w[g,n,k]) * (sa(r) * w_scales[g, n]),
+    fp32 (bf16 rounding is the caller's), with operand row A[r] = a[a_rows[r]]
+    and sa(r) = a_scales[a_rows[r]] (a_rows None: a[r], a_scales[r]).  The
+    integer sums are formed in float64, which is exact (|sum| <= 127^2 K <
+    2^53).  An identity group reads ident_a and ident_scales.  Rows outside
+    every group stay 0."""
     a = np.asarray(a, dtype=np.int8)
     w = np.asarray(w, dtype=np.int8)
     ws = np.asarray(w_scales, dtype=f32)
-    M = a.shape[0]
     rs = np.asarray(a_scales, dtype=f32)
-    if a_scale_idx is not None:
-        rs = rs[np.asarray(a_scale_idx, dtype=np.int64)]
+    if a_rows is not None:
+        sel = np.asarray(a_rows, dtype=np.int64)
+        a, rs = a[sel], rs[sel]
+    M = a.shape[0]
     out = np.zeros((M, w.shape[1]), dtype=f32)
     for g, (lo, hi) in enumerate(group_bounds(offs_incl, M)):
         if hi <= lo:

@@ -151,7 +151,7 @@ def test_grouped_gemm_validation():
 def test_int8_validation():
     L = M.lib()
     ws = ctypes.c_void_p(0x10000)
-    # a, a_scales, a_scale_idx, w, w_scales, offs, G, M, N, K, ident_a, ident_scales, ident_m,
+    # a, a_scales, a_rows, w, w_scales, offs, G, M, N, K, ident_a, ident_scales, ident_m,
     # out, ws, ws_bytes, stream
     args = lambda G=4, Mr=64, K=256, sc=FAKE, ia=None, isc=None, im=0, idx=None, wsb=4096: (
         FAKE, sc, idx, FAKE, FAKE, FAKE, G, Mr, 128, K, ia, isc, im, FAKE, ws, wsb, None)

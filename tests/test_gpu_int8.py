@@ -90,13 +90,31 @@ def test_grouped_gemm_i8_bit_exact(cuda, sizes, N, K):
     print("grouped_gemm_i8 sizes=%s N=%d K=%d" % (sizes, N, K), flush=True)
     out = torch.full((a.shape[0], N), 7.0, dtype=torch.bfloat16, device=cuda)
     t = lambda v: torch.from_numpy(v).to(cuda)
-    M.grouped_gemm_i8(t(a), t(rs), t(w), t(ws), inclusive(sizes, cuda), a_scale_idx=t(idx),
+    M.grouped_gemm_i8(t(a), t(rs), t(w), t(ws), inclusive(sizes, cuda), a_rows=t(idx),
                       out=out)
     torch.cuda.synchronize()
-    ref = bf16(O.grouped_gemm_i8(a, rs, w, ws, offs, a_scale_idx=idx))
+    ref = bf16(O.grouped_gemm_i8(a, rs, w, ws, offs, a_rows=idx))
     Mg = int(offs[-1])
     assert torch.equal(out[:Mg].cpu(), ref[:Mg])
     assert bool((out[Mg:] == 7.0).all())
+
+
+def test_grouped_gemm_i8_reads_rows_through_index(cuda):
+    """a is a 97-row token table; 1000 operand rows read it through a_rows
+    (as run() does with moe_permute's row_token instead of a gather)."""
+    rng = np.random.default_rng(21)
+    sizes, N, K, n_tok = [300, 0, 450, 250], 256, 384, 97
+    a = rng.integers(-127, 128, size=(n_tok, K)).astype(np.int8)
+    rs = (rng.random(n_tok) * 0.02 + 0.001).astype(np.float32)
+    rows = rng.integers(0, n_tok, size=sum(sizes)).astype(np.int32)
+    w = rng.integers(-127, 128, size=(len(sizes), N, K)).astype(np.int8)
+    ws = (rng.random((len(sizes), N)) * 0.02 + 0.001).astype(np.float32)
+    t = lambda v: torch.from_numpy(v).to(cuda)
+    out = M.grouped_gemm_i8(t(a), t(rs), t(w), t(ws), inclusive(sizes, cuda), a_rows=t(rows))
+    torch.cuda.synchronize()
+    assert out.shape == (sum(sizes), N)
+    ref = bf16(O.grouped_gemm_i8(a, rs, w, ws, np.cumsum(sizes), a_rows=rows))
+    assert torch.equal(out.cpu(), ref)
 
 
 def test_grouped_gemm_i8_identity_groups(cuda):
@@ -124,9 +142,9 @@ def test_grouped_swiglu_i8(cuda, sizes, N, K):
     t = lambda v: torch.from_numpy(v).to(cuda)
     print("grouped_swiglu_i8 sizes=%s N=%d K=%d" % (sizes, N, K), flush=True)
     h = M.grouped_swiglu_i8(t(a), t(rs), t(wg), t(wgs), t(wu), t(wus), inclusive(sizes, cuda),
-                            a_scale_idx=t(idx))
+                            a_rows=t(idx))
     torch.cuda.synchronize()
-    ref = O.grouped_swiglu_i8(a, rs, wg, wgs, wu, wus, np.cumsum(sizes), a_scale_idx=idx).double()
+    ref = O.grouped_swiglu_i8(a, rs, wg, wgs, wu, wus, np.cumsum(sizes), a_rows=idx).double()
     Mg = int(np.sum(sizes))
     got = h[:Mg].double().cpu()
     err = (got - ref[:Mg]).abs()

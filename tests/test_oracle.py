@@ -25,7 +25,7 @@ function is pinned here by something other than its own formula:
 | fwht_blocks           | scipy.linalg.hadamard (Sylvester) matrix product; H H = 128 I     |
 | quant_rows_i8         | hand rows (half-even ties, zero row, clamp); error <= s/2;        |
 |                       | rotated pair / 128 contracts to the unrotated product             |
-| grouped_gemm_i8       | brute-force Python integer loop; scale index / identity groups;  |
+| grouped_gemm_i8       | brute-force Python integer loop; row index / identity groups;    |
 |                       | dequantised float64 product                                      |
 """
 import itertools
@@ -464,7 +464,7 @@ def test_grouped_gemm_i8_brute_force():
     ident = rng.integers(-127, 128, size=(4, K)).astype(np.int8)
     ids = rng.random(4).astype(f32)
     offs = [3, 7, 9]                     # groups of 3, 4 (identity), 2 rows; rows 9-10 outside
-    got = O.grouped_gemm_i8(a, rs, w, ws, offs, a_scale_idx=idx, ident_a=ident,
+    got = O.grouped_gemm_i8(a, rs, w, ws, offs, a_rows=idx, ident_a=ident,
                             ident_scales=ids, ident_m=4)
     bounds = [(0, 3), (3, 7), (7, 9)]
     for r in range(M):
@@ -477,9 +477,9 @@ def test_grouped_gemm_i8_brute_force():
             if g == 1:
                 arow, sa = ident[r - 3], ids[r - 3]
             else:
-                arow, sa = a[r], rs[idx[r]]
+                arow, sa = a[idx[r]], rs[idx[r]]
             acc = sum(int(arow[k]) * int(w[g, n, k]) for k in range(K))
             assert got[r, n] == f32(acc) * (sa * ws[g, n])
     # against the dequantised float64 product
-    deq = (a.astype(np.float64) * rs[idx][:, None]) @ (w[0].astype(np.float64) * ws[0][:, None]).T
+    deq = (a[idx].astype(np.float64) * rs[idx][:, None]) @ (w[0].astype(np.float64) * ws[0][:, None]).T
     assert np.allclose(got[:3], deq[:3], rtol=1e-6, atol=1e-6)
