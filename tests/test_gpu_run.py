@@ -178,3 +178,33 @@ def test_run_int8_experts_small_shape(cuda):
     assert float((err <= 0.02 + 0.05 * acc.abs()).float().mean()) >= 0.99   # K:1640-1642
     with pytest.raises(RuntimeError):
         M.run(*dev_args, norm_min, experts="int8", dispatch="fp8")
+
+
+@pytest.mark.parametrize("B,S,zero_bias", [(1, 1, False), (2, 96, True), (1, 333, True)])
+def test_run_int8_experts_spread_routing_and_tiny_batch(cuda, B, S, zero_bias):
+    """run(..., experts="int8") where the routing does NOT collapse onto 8
+    whole experts (zero bias: groups of uneven size, rows read through
+    row_token) and at T = 1.  Against the CPU fp32 evaluation, harness gate
+    form at atol 0.02 (K:1640-1642)."""
+    hs, gw, bias, eg, eu, ed, sg, su, sd = make(B=B, S=S, seed=11)
+    if zero_bias:
+        bias = torch.zeros_like(bias)
+    norm_min = 1e-6
+    args = (hs, gw, bias, eg, eu, ed, sg, su, sd)
+    print("run int8 B=%d S=%d zero_bias=%s" % (B, S, zero_bias), flush=True)
+    out, logits = M.run(*[a.to(cuda) for a in args], norm_min, experts="int8")
+    torch.cuda.synchronize()
+    T, H = B * S, hs.shape[-1]
+    ids, wts = O.score_topk(logits.cpu().numpy(), bias.numpy(), 8,
+                            O.RouteCfg(O.SCORING_SOFTMAX_BIAS, norm_min=norm_min))
+    if zero_bias:
+        assert len(np.unique(ids)) > 8        # the groups really are spread
+    xf = hs.view(T, H).float()
+    acc = (torch.nn.functional.silu(xf @ sg.float().t()) * (xf @ su.float().t())) @ sd.float().t()
+    for t in range(T):
+        for j in range(8):
+            e = int(ids[t, j])
+            h = torch.nn.functional.silu(xf[t] @ eg[e].float().t()) * (xf[t] @ eu[e].float().t())
+            acc[t] += float(wts[t, j]) * (h @ ed[e].float().t())
+    err = (out.view(T, H).float().cpu() - acc).abs()
+    assert float((err <= 0.02 + 0.05 * acc.abs()).float().mean()) >= 0.99
