@@ -162,15 +162,16 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int A_INST = BM / ARPI, B_INST = BN / RPI, PER_WAVE = (A_INST + B_INST) / NW;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
-  static_assert(I8 ? BK == 128 : (BK == 32 || BK == 64), "K step of one or two MFMA depths");
+  static_assert(I8 ? (BK == 64 || BK == 128) : (BK == 32 || BK == 64), "K step of one or two MFMA depths");
   static_assert(!(I8 && AFP8), "int8 and fp8 A are separate paths");
   static_assert((A_INST + B_INST) % NW == 0, "every wave issues the same number of loads");
   static_assert(!AFP8 || BK == 64, "fp8 A: one 128-wide scale block spans two K steps");
   static_assert(!AFP8 || (BM * ACH) % NT == 0, "fp8 A: whole 16-byte chunks per thread per K step");
   static_assert(!SWIGLU || FN % 2 == 0, "swiglu: gate/up fragment pairs inside one wave");
-  static_assert(!PIPE || (!AFP8 && ROWB == 128 && NS == 2 && WM == 4 && WN == 2 && BM == 256),
-                "pipelined loop: bf16 / int8 A, 256-row tiles, 2 stages of 128-byte rows, "
-                "8 waves of 64 x 128");
+  static_assert(!PIPE || (!AFP8 && WM == 4 && WN == 2 && BM == 256 &&
+                          ((ROWB == 128 && NS == 2) || (ROWB == 64 && NS >= 3))),
+                "pipelined loops: bf16 / int8 A, 256-row tiles, 8 waves of 64 x 128; "
+                "2 stages of 128-byte rows, or 3+ stages of 64-byte rows");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B + DQ_BYTES];
   char* const dq = lds + NS * STAGE_B;
   const char* a = (const char*)a_;
@@ -286,14 +287,111 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = AccV{0, 0, 0, 0};
 
   const int KT = K / BK;
-  if constexpr (PIPE) {
-    // Software-pipelined K loop.  Per K step the wave reads its fragments in
-    // two halves (kk = 0, 1: 4 A + 8 B reads each).  The kk = 1 reads are
-    // issued before the kk = 0 MFMAs, and the next step's kk = 0 reads are
-    // issued right after the barrier, before the kk = 1 MFMAs.  The LDS
-    // latency thus hides behind MFMA work instead of stalling every step.
-    // The MFMA order per accumulator is the same as the plain loop's (K steps
-    // ascending, kk = 0 then 1), so the results are bit-identical to it.
+  if constexpr (PIPE && ROWB == 64) {
+    // Deep pipelined K loop: stages of one MFMA depth (64-byte rows), NS
+    // buffers, NS - 2 stages of DMA in flight behind the stage being read.
+    // Iteration kt:
+    //   wait until stage kt+1 landed (this wave), barrier (every wave: stage
+    //   kt+1 landed, and the reads of stage kt-1 are done);
+    //   DMA stage kt+NS-1 into stage kt-1's buffer;
+    //   issue the fragment reads of stage kt+1;
+    //   wait for stage kt's fragments (issued one iteration earlier), MFMAs.
+    // Each accumulator sees K in ascending order, one MFMA per stage: the
+    // results are bit-identical to the other loops.
+    constexpr int kFrag = 16 * ROWB;  // bytes between fragments (16 rows)
+    const unsigned l0 = lds_addr(lds);
+    const unsigned chunk = (unsigned)((fc ^ swz(fr, CH)) * 16);
+    const unsigned a_off = (wm * WTM + fr) * AROWB + chunk;
+    const unsigned b_off = A_BYTES + (wn * WTN + fr) * ROWB + chunk;
+    bf16x8 a0[FM], b0[FN], a1[FM], b1[FN];
+    auto read = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN], int st) {
+      const unsigned ab = l0 + st * STAGE_B + a_off, bb = l0 + st * STAGE_B + b_off;
+      MOE_DS_READ_B128(av[0], ab, 0 * kFrag);
+      MOE_DS_READ_B128(av[1], ab, 1 * kFrag);
+      MOE_DS_READ_B128(av[2], ab, 2 * kFrag);
+      MOE_DS_READ_B128(av[3], ab, 3 * kFrag);
+      MOE_DS_READ_B128(bv[0], bb, 0 * kFrag);
+      MOE_DS_READ_B128(bv[1], bb, 1 * kFrag);
+      MOE_DS_READ_B128(bv[2], bb, 2 * kFrag);
+      MOE_DS_READ_B128(bv[3], bb, 3 * kFrag);
+      MOE_DS_READ_B128(bv[4], bb, 4 * kFrag);
+      MOE_DS_READ_B128(bv[5], bb, 5 * kFrag);
+      MOE_DS_READ_B128(bv[6], bb, 6 * kFrag);
+      MOE_DS_READ_B128(bv[7], bb, 7 * kFrag);
+    };
+    static_assert(FM == 4 && FN == 8, "fragment reads written out for 64 x 128 wave tiles");
+    auto mma = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN]) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_step<I8>(av[i], bv[j], acc[i][j]);
+    };
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st)
+      if (st < KT) issue(st, st);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    if (!live) {
+      // DMA and barriers only, in the same order as the live loop below
+      int wst = NS - 1;  // buffer of stage kt + NS - 1
+      for (int kt = 0; kt < KT; ++kt) {
+        if (kt + NS - 2 < KT)
+          asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 3) * PER_WAVE) : "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kt + NS - 1 < KT) issue(kt + NS - 1, wst);
+        wst = wst + 1 == NS ? 0 : wst + 1;
+      }
+    } else {
+      read(a0, b0, 0);
+      int rst = 1;       // buffer of stage kt + 1
+      int wst = NS - 1;  // buffer of stage kt + NS - 1
+      for (int kt = 0; kt < KT; kt += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int k2 = kt + u;
+          if (k2 < KT) {
+            if (k2 + NS - 2 < KT)
+              asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 3) * PER_WAVE)
+                           : "memory");
+            else
+              asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            if (k2 + NS - 1 < KT) issue(k2 + NS - 1, wst);
+            const bool more = k2 + 1 < KT;
+            if (more) {
+              if (u == 0) read(a1, b1, rst);
+              else read(a0, b0, rst);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // the older half (this stage's fragments) landed
+            if (more) asm volatile("s_waitcnt lgkmcnt(12)" ::: "memory");
+            else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            if (u == 0) mma(a0, b0);
+            else mma(a1, b1);
+            __builtin_amdgcn_sched_barrier(0);
+            rst = rst + 1 == NS ? 0 : rst + 1;
+            wst = wst + 1 == NS ? 0 : wst + 1;
+          }
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  } else if constexpr (PIPE) {
+    // Software-pipelined K loop, two 128-byte-row stages, each K step in two
+    // halves (kk = 0, 1) with their own fragment registers F0 / F1.  The
+    // MFMAs of a half are interleaved with the LDS reads of the next half's
+    // fragments (one read after every second MFMA) and, in the kk = 1 half,
+    // with the DMA of the stage after next (one instruction after every
+    // fourth MFMA), so neither the LDS queue nor the DMA issue holds the
+    // matrix pipe.  Step s:
+    //   wait F0 (stage s, kk 0); MFMA(F0) + reads F1 (stage s, kk 1);
+    //   wait F1 and stage s+1's DMA (this wave); barrier (every wave: stage
+    //   s+1 landed, the reads of stage s done);
+    //   MFMA(F1) + reads F0 (stage s+1, kk 0) + DMA of stage s+2 into stage
+    //   s's buffer.
+    // Each accumulator sees K steps ascending, kk 0 then 1: bit-identical to
+    // the plain loop.
     const unsigned l0 = lds_addr(lds);
     unsigned abase[2][2], bbase[2][2];  // [stage][kk]: fragment 0; fragment i / j at +i*2048 / +j*2048
 #pragma unroll
@@ -305,26 +403,33 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
         bbase[st][kk] = l0 + st * STAGE_B + A_BYTES + (wn * WTN + fr) * ROWB + c;
       }
     bf16x8 a0[FM], b0[FN], a1[FM], b1[FN];
-    auto read = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN], unsigned ab, unsigned bb) {
-      MOE_DS_READ_B128(av[0], ab, 0);
-      MOE_DS_READ_B128(av[1], ab, 2048);
-      MOE_DS_READ_B128(av[2], ab, 4096);
-      MOE_DS_READ_B128(av[3], ab, 6144);
-      MOE_DS_READ_B128(bv[0], bb, 0);
-      MOE_DS_READ_B128(bv[1], bb, 2048);
-      MOE_DS_READ_B128(bv[2], bb, 4096);
-      MOE_DS_READ_B128(bv[3], bb, 6144);
-      MOE_DS_READ_B128(bv[4], bb, 8192);
-      MOE_DS_READ_B128(bv[5], bb, 10240);
-      MOE_DS_READ_B128(bv[6], bb, 12288);
-      MOE_DS_READ_B128(bv[7], bb, 14336);
+    auto read_one = [&](bf16x8& dst, unsigned addr) {
+      asm volatile("ds_read_b128 %0, %1" : "=v"(dst) : "v"(addr));
     };
-    auto mma = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN]) {
+    auto dma_one = [&](int q, int kt, int st) {
+      auto* dst = (__attribute__((address_space(3))) void*)(lds + st * STAGE_B +
+                                                            (wave * PER_WAVE + q) * 1024);
+      __builtin_amdgcn_global_load_lds((const void*)(src[q] + (long long)kt * kstep[q]), dst, 16,
+                                       0, 0);
+    };
+    constexpr int kReads = FM + FN;
+    static_assert(2 * kReads <= FM * FN && 4 * PER_WAVE <= FM * FN,
+                  "the reads and the DMA fit between the MFMAs of a half step");
+    // MFMAs on (av, bv); reads into (ra, rb) from (rab, rbb) when rd; DMA of
+    // stage dkt into buffer dst when dkt >= 0
+    auto half = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN], bf16x8 (&ra)[FM], bf16x8 (&rb)[FN],
+                    unsigned rab, unsigned rbb, bool rd, int dkt, int dst) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = mfma_step<I8>(av[i], bv[j], acc[i][j]);
+      for (int t = 0; t < FM * FN; ++t) {
+        acc[t / FN][t % FN] = mfma_step<I8>(av[t / FN], bv[t % FN], acc[t / FN][t % FN]);
+        if ((t & 1) && (t >> 1) < kReads && rd) {
+          const int r = t >> 1;
+          if (r < FM) read_one(ra[r], rab + r * 2048);
+          else read_one(rb[r - FM], rbb + (r - FM) * 2048);
+        }
+        if ((t & 3) == 2 && (t >> 2) < PER_WAVE && dkt >= 0) dma_one(t >> 2, dkt, dst);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     };
     issue(0, 0);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
@@ -336,30 +441,27 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
         if (k2 + 2 < KT) issue(k2 + 2, k2 & 1);
       }
     } else {
-    read(a0, b0, abase[0][0], bbase[0][0]);
-    for (int kt = 0; kt < KT; kt += 2) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int k2 = kt + u;  // stage k2 lives in buffer u
-        if (k2 < KT) {
-          read(a1, b1, abase[u][1], bbase[u][1]);
-          __builtin_amdgcn_sched_barrier(0);
-          asm volatile("s_waitcnt lgkmcnt(12)" ::: "memory");  // a0 / b0 (the older 12) landed
-          __builtin_amdgcn_sched_barrier(0);
-          mma(a0, b0);
-          __builtin_amdgcn_sched_barrier(0);
-          // this wave's reads of stage k2 and its DMA of stage k2 + 1 are done;
-          // the barrier makes that true for every wave
-          asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-          __builtin_amdgcn_sched_barrier(0);
-          if (k2 + 2 < KT) issue(k2 + 2, u);
-          if (k2 + 1 < KT) read(a0, b0, abase[u ^ 1][0], bbase[u ^ 1][0]);
-          __builtin_amdgcn_sched_barrier(0);
-          mma(a1, b1);
-          __builtin_amdgcn_sched_barrier(0);
+      for (int r = 0; r < FM; ++r) read_one(a0[r], abase[0][0] + r * 2048);
+#pragma unroll
+      for (int r = 0; r < FN; ++r) read_one(b0[r], bbase[0][0] + r * 2048);
+      for (int kt = 0; kt < KT; kt += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int k2 = kt + u;  // stage k2 lives in buffer u
+          if (k2 < KT) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // F0 of stage k2
+            __builtin_amdgcn_sched_barrier(0);
+            half(a0, b0, a1, b1, abase[u][1], bbase[u][1], true, -1, 0);
+            // F1 landed (this wave's reads of stage k2 are done) and stage
+            // k2+1's DMA landed; the barrier makes both true for every wave
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            half(a1, b1, a0, b0, abase[u ^ 1][0], bbase[u ^ 1][0], k2 + 1 < KT,
+                 k2 + 2 < KT ? k2 + 2 : -1, u);
+          }
         }
       }
-    }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   } else {
@@ -522,12 +624,12 @@ int grouped_gemm_n_tiles(int N, bool swiglu) {
   return (N + per - 1) / per;
 }
 
-template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS, bool I8 = false>
+template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS, bool I8 = false, int BKE = 0>
 static hipError_t launch_gg(const void* a, const float* a_scales, const void* ident_a, int ident_m,
                             const void* w0, const void* w1, const int32_t* offs, int G, int M, int N,
                             int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s,
                             I8Scales i8s = I8Scales{}) {
-  constexpr int BK = I8 ? 128 : 64;
+  constexpr int BK = BKE ? BKE : (I8 ? 128 : 64);  // K-step elements
   hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, BM, tile_start);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
