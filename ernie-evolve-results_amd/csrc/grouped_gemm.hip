@@ -121,11 +121,6 @@ __device__ __forceinline__ typename AccOf<I8>::type mfma_step(bf16x8 a, bf16x8 b
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
 }
-// One 16-byte LDS fragment read issued as an instruction the compiler does not
-// track: the pipelined loop below places its own lgkmcnt waits, which lets a
-// K step's fragment reads stay in flight across the next MFMA group.
-#define MOE_DS_READ_B128(dst, addr, off) \
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(off))
 
 // Row / column scales of the int8 operands (unused by the bf16 and fp8 paths).
 struct I8Scales {
@@ -162,16 +157,15 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   constexpr int NW = WM * WN, NT = 64 * NW;
   constexpr int A_INST = BM / ARPI, B_INST = BN / RPI, PER_WAVE = (A_INST + B_INST) / NW;
   constexpr int WTM = BM / WM, WTN = BN / WN, FM = WTM / 16, FN = WTN / 16;
-  static_assert(I8 ? (BK == 64 || BK == 128) : (BK == 32 || BK == 64), "K step of one or two MFMA depths");
+  static_assert(I8 ? BK == 128 : (BK == 32 || BK == 64), "K step of one or two MFMA depths");
   static_assert(!(I8 && AFP8), "int8 and fp8 A are separate paths");
   static_assert((A_INST + B_INST) % NW == 0, "every wave issues the same number of loads");
   static_assert(!AFP8 || BK == 64, "fp8 A: one 128-wide scale block spans two K steps");
   static_assert(!AFP8 || (BM * ACH) % NT == 0, "fp8 A: whole 16-byte chunks per thread per K step");
   static_assert(!SWIGLU || FN % 2 == 0, "swiglu: gate/up fragment pairs inside one wave");
-  static_assert(!PIPE || (!AFP8 && WM == 4 && WN == 2 && BM == 256 &&
-                          ((ROWB == 128 && NS == 2) || (ROWB == 64 && NS >= 3))),
-                "pipelined loops: bf16 / int8 A, 256-row tiles, 8 waves of 64 x 128; "
-                "2 stages of 128-byte rows, or 3+ stages of 64-byte rows");
+  static_assert(!PIPE || (!AFP8 && ROWB == 128 && NS == 2 && WM == 4 && WN == 2 && BM == 256),
+                "pipelined loop: bf16 / int8 A, 256-row tiles, 2 stages of 128-byte rows, "
+                "8 waves of 64 x 128");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B + DQ_BYTES];
   char* const dq = lds + NS * STAGE_B;
   const char* a = (const char*)a_;
@@ -287,97 +281,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     for (int j = 0; j < FN; ++j) acc[i][j] = AccV{0, 0, 0, 0};
 
   const int KT = K / BK;
-  if constexpr (PIPE && ROWB == 64) {
-    // Deep pipelined K loop: stages of one MFMA depth (64-byte rows), NS
-    // buffers, NS - 2 stages of DMA in flight behind the stage being read.
-    // Iteration kt:
-    //   wait until stage kt+1 landed (this wave), barrier (every wave: stage
-    //   kt+1 landed, and the reads of stage kt-1 are done);
-    //   DMA stage kt+NS-1 into stage kt-1's buffer;
-    //   issue the fragment reads of stage kt+1;
-    //   wait for stage kt's fragments (issued one iteration earlier), MFMAs.
-    // Each accumulator sees K in ascending order, one MFMA per stage: the
-    // results are bit-identical to the other loops.
-    constexpr int kFrag = 16 * ROWB;  // bytes between fragments (16 rows)
-    const unsigned l0 = lds_addr(lds);
-    const unsigned chunk = (unsigned)((fc ^ swz(fr, CH)) * 16);
-    const unsigned a_off = (wm * WTM + fr) * AROWB + chunk;
-    const unsigned b_off = A_BYTES + (wn * WTN + fr) * ROWB + chunk;
-    bf16x8 a0[FM], b0[FN], a1[FM], b1[FN];
-    auto read = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN], int st) {
-      const unsigned ab = l0 + st * STAGE_B + a_off, bb = l0 + st * STAGE_B + b_off;
-      MOE_DS_READ_B128(av[0], ab, 0 * kFrag);
-      MOE_DS_READ_B128(av[1], ab, 1 * kFrag);
-      MOE_DS_READ_B128(av[2], ab, 2 * kFrag);
-      MOE_DS_READ_B128(av[3], ab, 3 * kFrag);
-      MOE_DS_READ_B128(bv[0], bb, 0 * kFrag);
-      MOE_DS_READ_B128(bv[1], bb, 1 * kFrag);
-      MOE_DS_READ_B128(bv[2], bb, 2 * kFrag);
-      MOE_DS_READ_B128(bv[3], bb, 3 * kFrag);
-      MOE_DS_READ_B128(bv[4], bb, 4 * kFrag);
-      MOE_DS_READ_B128(bv[5], bb, 5 * kFrag);
-      MOE_DS_READ_B128(bv[6], bb, 6 * kFrag);
-      MOE_DS_READ_B128(bv[7], bb, 7 * kFrag);
-    };
-    static_assert(FM == 4 && FN == 8, "fragment reads written out for 64 x 128 wave tiles");
-    auto mma = [&](bf16x8 (&av)[FM], bf16x8 (&bv)[FN]) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma_step<I8>(av[i], bv[j], acc[i][j]);
-    };
-#pragma unroll
-    for (int st = 0; st < NS - 1; ++st)
-      if (st < KT) issue(st, st);
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if (!live) {
-      // DMA and barriers only, in the same order as the live loop below
-      int wst = NS - 1;  // buffer of stage kt + NS - 1
-      for (int kt = 0; kt < KT; ++kt) {
-        if (kt + NS - 2 < KT)
-          asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 3) * PER_WAVE) : "memory");
-        else
-          asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-        if (kt + NS - 1 < KT) issue(kt + NS - 1, wst);
-        wst = wst + 1 == NS ? 0 : wst + 1;
-      }
-    } else {
-      read(a0, b0, 0);
-      int rst = 1;       // buffer of stage kt + 1
-      int wst = NS - 1;  // buffer of stage kt + NS - 1
-      for (int kt = 0; kt < KT; kt += 2) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int k2 = kt + u;
-          if (k2 < KT) {
-            if (k2 + NS - 2 < KT)
-              asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"((NS - 3) * PER_WAVE)
-                           : "memory");
-            else
-              asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
-            if (k2 + NS - 1 < KT) issue(k2 + NS - 1, wst);
-            const bool more = k2 + 1 < KT;
-            if (more) {
-              if (u == 0) read(a1, b1, rst);
-              else read(a0, b0, rst);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            // the older half (this stage's fragments) landed
-            if (more) asm volatile("s_waitcnt lgkmcnt(12)" ::: "memory");
-            else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
-            if (u == 0) mma(a0, b0);
-            else mma(a1, b1);
-            __builtin_amdgcn_sched_barrier(0);
-            rst = rst + 1 == NS ? 0 : rst + 1;
-            wst = wst + 1 == NS ? 0 : wst + 1;
-          }
-        }
-      }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  } else if constexpr (PIPE) {
+  if constexpr (PIPE) {
     // Software-pipelined K loop, two 128-byte-row stages, each K step in two
     // halves (kk = 0, 1) with their own fragment registers F0 / F1.  The
     // MFMAs of a half are interleaved with the LDS reads of the next half's
@@ -403,6 +307,9 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
         bbase[st][kk] = l0 + st * STAGE_B + A_BYTES + (wn * WTN + fr) * ROWB + c;
       }
     bf16x8 a0[FM], b0[FN], a1[FM], b1[FN];
+    // One 16-byte LDS fragment read issued as an instruction the compiler does
+    // not track: the loop places its own lgkmcnt waits, so the reads stay in
+    // flight across the MFMAs they are interleaved with.
     auto read_one = [&](bf16x8& dst, unsigned addr) {
       asm volatile("ds_read_b128 %0, %1" : "=v"(dst) : "v"(addr));
     };
@@ -624,12 +531,12 @@ int grouped_gemm_n_tiles(int N, bool swiglu) {
   return (N + per - 1) / per;
 }
 
-template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS, bool I8 = false, int BKE = 0>
+template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS, bool I8 = false>
 static hipError_t launch_gg(const void* a, const float* a_scales, const void* ident_a, int ident_m,
                             const void* w0, const void* w1, const int32_t* offs, int G, int M, int N,
                             int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s,
                             I8Scales i8s = I8Scales{}) {
-  constexpr int BK = BKE ? BKE : (I8 ? 128 : 64);  // K-step elements
+  constexpr int BK = I8 ? 128 : 64;  // K-step elements
   hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, BM, tile_start);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
