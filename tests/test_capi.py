@@ -188,6 +188,22 @@ def test_python_layer_refuses_cpu_tensors():
         M.router_gemm(x, x)
     with pytest.raises(RuntimeError, match="no CPU path"):
         M.permute(x, torch.zeros(4, 2, dtype=torch.int32), 8)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        M.quant_rows_i8(x)
+
+
+def test_run_rejects_bad_options():
+    """run()'s keyword options are checked before any device work."""
+    hs = torch.zeros(1, 4, 64, dtype=torch.bfloat16)
+    args = (hs,) + (None,) * 8 + (1e-6,)
+    with pytest.raises(RuntimeError, match="dispatch"):
+        M.run(*args, dispatch="int4")
+    with pytest.raises(RuntimeError, match="experts"):
+        M.run(*args, experts="fp4")
+    with pytest.raises(RuntimeError, match="dispatch must stay"):
+        M.run(*args, experts="int8", dispatch="fp8")
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        M.run(*args, experts="int8")
 
 
 def test_missing_library_raises(monkeypatch):
