@@ -122,9 +122,10 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
 }
 
-// Row / column scales of the int8 operands (unused by the bf16 and fp8 paths).
-struct I8Scales {
-  const float* a;      // per row of a
+// The A operand's row map (bf16 and int8 A) and the row / column scales of the
+// int8 operands (unused by the bf16 and fp8 paths).
+struct GgExtra {
+  const float* a;      // int8: per row of a
   const int* a_idx;    // NULL, or [M]: operand row r is row a_idx[r] of a (data and scale)
   const float* ident;  // [ident_m] per row of ident_a
   const float* w0;     // [G, N] per weight row of w0
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     const void* __restrict__ a_, const float* __restrict__ a_scales, const void* __restrict__ ident_,
     int ident_m, const void* __restrict__ w0_, const void* __restrict__ w1_,
     const int* __restrict__ offs, const int* __restrict__ tile_start, int G, int M, int N, int K,
-    int n_tiles, unsigned short* __restrict__ out, I8Scales i8s) {
+    int n_tiles, unsigned short* __restrict__ out, GgExtra i8s) {
   // LDS rows: B (weights) BK*WEL bytes; A BK*2 bytes (bf16) or BK bytes (fp8,
   // int8).  bf16 steps are 64 wide, int8 steps 128 wide: 128-byte rows either
   // way.  A DMA wave instruction moves 1 KB = 1024 / row-bytes rows.
@@ -225,8 +226,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     if (gi < A_INST) {
       const int r = gi * ARPI + lane / ACH, p = lane % ACH;
       const int row = min(r0 + r, rlast);  // rows past the group are loaded, never stored
-      int arow_i = row;
-      if constexpr (I8) arow_i = (!ident && i8s.a_idx) ? i8s.a_idx[row] : row;
+      const int arow_i = (!ident && i8s.a_idx) ? i8s.a_idx[row] : row;
       const char* arow = ident ? ident_a + (long long)(row - gs) * K * AEL
                                : a + (long long)arow_i * K * AEL;
       src[q] = arow + (p ^ swz(r, ACH)) * 16;
@@ -535,7 +535,7 @@ template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS, bool I8 = false>
 static hipError_t launch_gg(const void* a, const float* a_scales, const void* ident_a, int ident_m,
                             const void* w0, const void* w1, const int32_t* offs, int G, int M, int N,
                             int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s,
-                            I8Scales i8s = I8Scales{}) {
+                            GgExtra i8s = GgExtra{}) {
   constexpr int BK = I8 ? 128 : 64;  // K-step elements
   hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, BM, tile_start);
   hipError_t e = hipGetLastError();
@@ -559,11 +559,13 @@ static hipError_t launch_gg(const void* a, const float* a_scales, const void* id
 
 // tile_start: [G+1] ints of workspace.  offs: inclusive group ends (device).
 // a_scales == NULL: a is bf16.  Else a is e4m3fn bytes with one fp32 scale per
-// row and 128-wide K block ([M, K/128]).
-hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const void* ident_a,
-                               int ident_m, const void* w0, const void* w1, const int32_t* offs,
-                               int G, int M, int N, int K, bool swiglu, void* out,
-                               int32_t* tile_start, hipStream_t s) {
+// row and 128-wide K block ([M, K/128]).  a_rows (bf16 A only; may be NULL):
+// operand row r is row a_rows[r] of a.
+hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const int32_t* a_rows,
+                               const void* ident_a, int ident_m, const void* w0, const void* w1,
+                               const int32_t* offs, int G, int M, int N, int K, bool swiglu,
+                               void* out, int32_t* tile_start, hipStream_t s) {
+  const GgExtra ex{nullptr, a_rows, nullptr, nullptr, nullptr};
   // fp8 A (its dequantisation pass needs a barrier inside each K step): 256-row
   // tiles, 16 waves of 64 x 64, the plain loop.
   if (a_scales)
@@ -575,11 +577,11 @@ hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const void*
   // measured 7-16% faster at T = 1571, 10% slower at T = 8192.
   if ((long long)M <= 320ll * G)
     return launch_gg<false, 2, 8, false, 128, 3>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M,
-                                                 N, K, swiglu, out, tile_start, s);
+                                                 N, K, swiglu, out, tile_start, s, ex);
   // bf16 A, larger groups: 256-row tiles, 8 waves of 64 x 128 accumulators,
   // the software-pipelined K loop.
   return launch_gg<false, 4, 2, true, 256, 2>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M, N,
-                                              K, swiglu, out, tile_start, s);
+                                              K, swiglu, out, tile_start, s, ex);
 }
 
 // int8 A and weights, int32 accumulation, 128-wide K steps: the same tile
@@ -589,7 +591,7 @@ hipError_t launch_grouped_gemm_i8(const void* a, const float* a_rs, const int32_
                                   const void* w0, const float* w0s, const void* w1,
                                   const float* w1s, const int32_t* offs, int G, int M, int N, int K,
                                   bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
-  const I8Scales sc{a_rs, a_rs_idx, ident_rs, w0s, swiglu ? w1s : w0s};
+  const GgExtra sc{a_rs, a_rs_idx, ident_rs, w0s, swiglu ? w1s : w0s};
   if ((long long)M <= 320ll * G)
     return launch_gg<false, 2, 8, false, 128, 3, true>(a, nullptr, ident_a, ident_m, w0, w1, offs,
                                                        G, M, N, K, swiglu, out, tile_start, s, sc);

@@ -272,10 +272,10 @@ size_t moe_grouped_gemm_workspace_bytes(int G) {
   return round256((size_t)(G + 1) * 4);
 }
 
-static int grouped_common(const void* a, const float* a_scales, const void* w0, const void* w1,
-                          const int32_t* offs, int G, int M, int N, int K, const void* ident_a,
-                          int ident_m, void* out, void* ws, size_t ws_bytes, void* stream,
-                          bool swiglu, bool fp8) {
+static int grouped_common(const void* a, const float* a_scales, const int32_t* a_rows,
+                          const void* w0, const void* w1, const int32_t* offs, int G, int M,
+                          int N, int K, const void* ident_a, int ident_m, void* out, void* ws,
+                          size_t ws_bytes, void* stream, bool swiglu, bool fp8, bool rows) {
   if (G < 1 || G > 65536) return fail(MOE_ERR_INVALID_ARG, "G=%d not in [1, 65536]", G);
   if (M < 0 || N < 1 || K < 1) return fail(MOE_ERR_INVALID_ARG, "M=%d, N=%d, K=%d", M, N, K);
   if (K % 64 != 0) return fail(MOE_ERR_UNSUPPORTED, "K=%d is not a multiple of 64", K);
@@ -294,6 +294,9 @@ static int grouped_common(const void* a, const float* a_scales, const void* w0, 
   if (M > 0 && (!a || !w0 || !w1 || !out))
     return fail(MOE_ERR_NULL_POINTER, "a, the weights and the output are required");
   if (ident_m > 0 && !ident_a) return fail(MOE_ERR_NULL_POINTER, "ident_m > 0 needs ident_a");
+  if (rows && M > 0 && !a_rows) return fail(MOE_ERR_NULL_POINTER, "a_rows is required");
+  if (a_rows && ((uintptr_t)a_rows & 3u))
+    return fail(MOE_ERR_ALIGNMENT, "a_rows not 4-byte aligned");
   if ((a && !aligned16(a)) || (w0 && !aligned16(w0)) || (w1 && !aligned16(w1)) ||
       (ident_a && !aligned16(ident_a)))
     return fail(MOE_ERR_ALIGNMENT, "a, ident_a and the weights must be 16-byte aligned");
@@ -307,8 +310,8 @@ static int grouped_common(const void* a, const float* a_scales, const void* w0, 
   const long long blocks = (((long long)M + 127) / 128 + G) *
                            moe::grouped_gemm_n_tiles(N, swiglu);
   if (blocks >= (1ll << 31)) return fail(MOE_ERR_UNSUPPORTED, "too many tiles (%lld)", blocks);
-  return launched(moe::launch_grouped_gemm(a, fp8 ? a_scales : nullptr, ident_a, ident_m, w0, w1,
-                                           offs, G, M, N, K, swiglu, out, (int32_t*)ws,
+  return launched(moe::launch_grouped_gemm(a, fp8 ? a_scales : nullptr, a_rows, ident_a, ident_m,
+                                           w0, w1, offs, G, M, N, K, swiglu, out, (int32_t*)ws,
                                            (hipStream_t)stream),
                   swiglu ? "grouped_swiglu" : "grouped_gemm");
 }
@@ -316,29 +319,43 @@ static int grouped_common(const void* a, const float* a_scales, const void* w0, 
 int moe_grouped_gemm(const void* a, const void* w, const int32_t* offs, int G, int M, int N,
                      int K, const void* ident_a, int ident_m, void* out, void* ws,
                      size_t ws_bytes, void* stream) {
-  return grouped_common(a, nullptr, w, w, offs, G, M, N, K, ident_a, ident_m, out, ws, ws_bytes,
-                        stream, false, false);
+  return grouped_common(a, nullptr, nullptr, w, w, offs, G, M, N, K, ident_a, ident_m, out, ws,
+                        ws_bytes, stream, false, false, false);
 }
 
 int moe_grouped_swiglu(const void* a, const void* wg, const void* wu, const int32_t* offs,
                        int G, int M, int N, int K, const void* ident_a, int ident_m, void* h,
                        void* ws, size_t ws_bytes, void* stream) {
-  return grouped_common(a, nullptr, wg, wu, offs, G, M, N, K, ident_a, ident_m, h, ws, ws_bytes,
-                        stream, true, false);
+  return grouped_common(a, nullptr, nullptr, wg, wu, offs, G, M, N, K, ident_a, ident_m, h, ws,
+                        ws_bytes, stream, true, false, false);
+}
+
+int moe_grouped_gemm_rows(const void* a, const int32_t* a_rows, const void* w,
+                          const int32_t* offs, int G, int M, int N, int K, void* out, void* ws,
+                          size_t ws_bytes, void* stream) {
+  return grouped_common(a, nullptr, a_rows, w, w, offs, G, M, N, K, nullptr, 0, out, ws,
+                        ws_bytes, stream, false, false, true);
+}
+
+int moe_grouped_swiglu_rows(const void* a, const int32_t* a_rows, const void* wg, const void* wu,
+                            const int32_t* offs, int G, int M, int N, int K, void* h, void* ws,
+                            size_t ws_bytes, void* stream) {
+  return grouped_common(a, nullptr, a_rows, wg, wu, offs, G, M, N, K, nullptr, 0, h, ws,
+                        ws_bytes, stream, true, false, true);
 }
 
 int moe_grouped_gemm_fp8(const void* a, const float* a_scales, const void* w, const int32_t* offs,
                          int G, int M, int N, int K, void* out, void* ws, size_t ws_bytes,
                          void* stream) {
-  return grouped_common(a, a_scales, w, w, offs, G, M, N, K, nullptr, 0, out, ws, ws_bytes,
-                        stream, false, true);
+  return grouped_common(a, a_scales, nullptr, w, w, offs, G, M, N, K, nullptr, 0, out, ws,
+                        ws_bytes, stream, false, true, false);
 }
 
 int moe_grouped_swiglu_fp8(const void* a, const float* a_scales, const void* wg, const void* wu,
                            const int32_t* offs, int G, int M, int N, int K, void* h, void* ws,
                            size_t ws_bytes, void* stream) {
-  return grouped_common(a, a_scales, wg, wu, offs, G, M, N, K, nullptr, 0, h, ws, ws_bytes,
-                        stream, true, true);
+  return grouped_common(a, a_scales, nullptr, wg, wu, offs, G, M, N, K, nullptr, 0, h, ws,
+                        ws_bytes, stream, true, true, false);
 }
 
 static int grouped_i8_common(const int8_t* a, const float* a_scales, const int32_t* a_rows,

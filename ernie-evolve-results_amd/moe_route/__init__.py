@@ -33,7 +33,8 @@ EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
            "moe_permute_workspace_bytes", "moe_permute", "moe_combine",
            "moe_grouped_gemm_workspace_bytes", "moe_grouped_gemm", "moe_grouped_swiglu",
            "moe_grouped_gemm_fp8", "moe_grouped_swiglu_fp8", "moe_quant_rows_i8",
-           "moe_grouped_gemm_i8", "moe_grouped_swiglu_i8"]
+           "moe_grouped_gemm_i8", "moe_grouped_swiglu_i8", "moe_grouped_gemm_rows",
+           "moe_grouped_swiglu_rows"]
 
 
 class MoeError(RuntimeError):
@@ -95,6 +96,10 @@ def lib():
         L.moe_grouped_gemm_fp8.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _Z, _P]
         L.moe_grouped_swiglu_fp8.restype = _I
         L.moe_grouped_swiglu_fp8.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _Z, _P]
+        L.moe_grouped_gemm_rows.restype = _I
+        L.moe_grouped_gemm_rows.argtypes = [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _Z, _P]
+        L.moe_grouped_swiglu_rows.restype = _I
+        L.moe_grouped_swiglu_rows.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _Z, _P]
         L.moe_quant_rows_i8.restype = _I
         L.moe_quant_rows_i8.argtypes = [_P, ctypes.c_longlong, _I, _I, _F, _I, _P, _P, _P, _P]
         L.moe_grouped_gemm_i8.restype = _I
@@ -270,32 +275,57 @@ def _grouped_args(a, offs, ident_a, ident_m, fp8=False):
     return ws
 
 
-def grouped_gemm(a, w, offs, ident_a=None, ident_m=0, out=None):
+def _rows_arg(a_rows, ident_a):
+    if a_rows is None:
+        return None
+    _dev(a_rows, "a_rows")
+    if a_rows.dtype != torch.int32:
+        raise RuntimeError("a_rows must be int32")
+    if ident_a is not None:
+        raise RuntimeError("a_rows and ident_a are exclusive")
+    return a_rows
+
+
+def grouped_gemm(a, w, offs, ident_a=None, ident_m=0, out=None, a_rows=None):
     """Expert grouped GEMM (the reference's grouped_mm, moe_gemm.h:66-85):
-    out[r] = a[r] . w[g]^T for the rows r of group g = [offs[g-1], offs[g]).
-    a [M,K] bf16, w [G,N,K] bf16, offs [G] int32 INCLUSIVE ends (moe_permute's
-    offsets[1:]); returns out [M,N] bf16.  Rows outside every group are not
-    written."""
+    out[r] = A[r] . w[g]^T for the rows r of group g = [offs[g-1], offs[g]).
+    A[r] = a[r], or a[a_rows[r]] with a row map (moe_grouped_gemm_rows: the
+    gather read through moe_permute's row_token).  a bf16 [rows, K], w
+    [G,N,K] bf16, offs [G] int32 INCLUSIVE ends (moe_permute's offsets[1:]);
+    returns out [M,N] bf16, M = len(a_rows) or a's rows.  Rows outside every
+    group are not written."""
     ws = _grouped_args(a, offs, ident_a, ident_m)
+    a_rows = _rows_arg(a_rows, ident_a)
     G, N, K = w.shape
-    M = a.shape[0]
+    M = a_rows.numel() if a_rows is not None else a.shape[0]
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    if a_rows is not None:
+        _check(lib().moe_grouped_gemm_rows(_ptr(a), _ptr(a_rows), _ptr(w), _ptr(offs), G, M, N,
+                                           K, _ptr(out), _ptr(ws), ws.numel(), _stream(a)))
+        return out
     _check(lib().moe_grouped_gemm(_ptr(a), _ptr(w), _ptr(offs), G, M, N, K, _ptr(ident_a),
                                   int(ident_m), _ptr(out), _ptr(ws), ws.numel(), _stream(a)))
     return out
 
 
-def grouped_swiglu(a, wg, wu, offs, ident_a=None, ident_m=0, out=None):
+def grouped_swiglu(a, wg, wu, offs, ident_a=None, ident_m=0, out=None, a_rows=None):
     """SwiGLU expert projection (grouped_mm_pair, moe_gemm.h:87-95, plus the
-    silu*mul): h[r] = silu(a[r] . wg[g]^T) * (a[r] . wu[g]^T), bf16 [M,N]."""
+    silu*mul): h[r] = silu(A[r] . wg[g]^T) * (A[r] . wu[g]^T), bf16 [M,N];
+    A[r] as in grouped_gemm."""
     ws = _grouped_args(a, offs, ident_a, ident_m)
+    a_rows = _rows_arg(a_rows, ident_a)
     if wg.shape != wu.shape:
         raise RuntimeError("gate and up weights must have one shape")
     G, N, K = wg.shape
-    M = a.shape[0]
+    M = a_rows.numel() if a_rows is not None else a.shape[0]
     if out is None:
         out = torch.empty(M, N, dtype=torch.bfloat16, device=a.device)
+    if a_rows is not None:
+        _check(lib().moe_grouped_swiglu_rows(_ptr(a), _ptr(a_rows), _ptr(wg), _ptr(wu),
+                                             _ptr(offs), G, M, N, K, _ptr(out), _ptr(ws),
+                                             ws.numel(), _stream(a)))
+        return out
     _check(lib().moe_grouped_swiglu(_ptr(a), _ptr(wg), _ptr(wu), _ptr(offs), G, M, N, K,
                                     _ptr(ident_a), int(ident_m), _ptr(out), _ptr(ws), ws.numel(),
                                     _stream(a)))
@@ -439,7 +469,9 @@ def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, e
     host synchronisation:
       routing   fp32 gate_weight hi/lo split, softmax + post-softmax bias,
                 top-8, w = c / max(sum c, norm_min)  (K:1786-1920);
-      dispatch  stable expert-major permutation + row gather (K:1922-2238);
+      dispatch  stable expert-major permutation (K:1922-2238); the expert
+                GEMM reads each routed row of x through row_token instead of
+                a gathered copy (K:2216-2230's gather, fused);
       experts   h = silu(xg . Wg[e]^T) * (xg . Wu[e]^T), y = h . Wd[e]^T as two
                 grouped GEMMs over the device offsets (the reference's CUTLASS
                 grouped GEMMs, moe_gemm.h:66-95);
@@ -485,12 +517,15 @@ def run(hidden_states, gate_weight, e_score_correction_bias, expert_gate_proj, e
 
 
 def _experts_bf16(x, ids, E, dispatch, wg, wu, wd):
-    p = permute(x, ids, E, fp8=dispatch == "fp8")
-    ends = p["offsets"][1:]  # inclusive group ends (moe_gemm.h:66-69)
     if dispatch == "fp8":
+        p = permute(x, ids, E, fp8=True)
+        ends = p["offsets"][1:]  # inclusive group ends (moe_gemm.h:66-69)
         h = grouped_swiglu_fp8(p["xg"], p["scales"], wg, wu, ends)
     else:
-        h = grouped_swiglu(p["xg"], wg, wu, ends)
+        # index-only permute: the gate+up GEMM reads token rows through row_token
+        p = permute(x, ids, E, index_only=True)
+        ends = p["offsets"][1:]
+        h = grouped_swiglu(x, wg, wu, ends, a_rows=p["row_token"])
     return grouped_gemm(h, wd, ends), p
 
 

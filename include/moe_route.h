@@ -165,6 +165,19 @@ int moe_grouped_swiglu(const void* a, const void* wg, const void* wu, const int3
                        int G, int M, int N, int K, const void* ident_a, int ident_m, void* h,
                        void* ws, size_t ws_bytes, void* stream);
 
+/* The same two GEMMs with a row map instead of gathered rows: operand row r is
+ * row a_rows[r] of a (e.g. a = the tokens x and a_rows = moe_permute's
+ * row_token, so the permute runs index-only and no gathered copy is
+ * written).  This generalises the reference plan's identity shortcut, which
+ * aims A at x when a group holds all T tokens (moe_gemm.cu:616-650), to any
+ * group.  a_rows [M] int32 (values must be rows of a), out / h [M, N]. */
+int moe_grouped_gemm_rows(const void* a, const int32_t* a_rows, const void* w,
+                          const int32_t* offs, int G, int M, int N, int K, void* out, void* ws,
+                          size_t ws_bytes, void* stream);
+int moe_grouped_swiglu_rows(const void* a, const int32_t* a_rows, const void* wg, const void* wu,
+                            const int32_t* offs, int G, int M, int N, int K, void* h, void* ws,
+                            size_t ws_bytes, void* stream);
+
 /* fp8 dispatch into the expert GEMMs: the A operand is moe_permute's fp8
  * output (e4m3fn bytes a [M, K] plus fp32 scales a_scales [M, K/128]) and is
  * dequantised in the GEMM's A load as bf16(q * s) -- the fp8 row permute

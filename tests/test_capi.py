@@ -143,6 +143,12 @@ def test_grouped_gemm_validation():
                                  FAKE, ws, 4096, None), -6)
     err(L.moe_grouped_gemm_fp8(FAKE, FAKE, FAKE, FAKE, 4, 1 << 24, 128, 1 << 14, FAKE, ws, 4096,
                                None), -3, "int32")
+    # a, a_rows, w, offs, G, M, N, K, out, ws, ws_bytes, stream
+    err(L.moe_grouped_gemm_rows(FAKE, None, FAKE, FAKE, 4, 64, 128, 256, FAKE, ws, 4096, None), -1,
+        "a_rows")
+    err(L.moe_grouped_swiglu_rows(FAKE, ctypes.c_void_p(0x10002), FAKE, FAKE, FAKE, 4, 64, 128,
+                                  256, FAKE, ws, 4096, None), -6, "a_rows")
+    err(L.moe_grouped_gemm_rows(FAKE, FAKE, FAKE, FAKE, 4, 64, 128, 100, FAKE, ws, 4096, None), -3)
     assert L.moe_grouped_gemm_workspace_bytes(64) == 512
     assert L.moe_grouped_gemm_workspace_bytes(0) == 256
     assert L.moe_grouped_gemm_workspace_bytes(-1) == 0

@@ -251,3 +251,30 @@ def test_fp8_permute_feeds_grouped_gemm(cuda):
     torch.cuda.synchronize()
     assert torch.equal(p["xg"].cpu().view(torch.uint8), q.view(torch.uint8))
     assert torch.equal(h8, h16)
+
+
+@pytest.mark.parametrize("sizes,N,K", [
+    ([30, 0, 200, 77], 256, 512),        # small groups: 128-row tiles
+    ([700, 1, 900], 320, 384),           # large groups: pipelined, odd K steps
+])
+def test_grouped_rows_equal_gathered_rows(cuda, sizes, N, K):
+    """moe_grouped_gemm_rows / moe_grouped_swiglu_rows read operand row r as
+    a[a_rows[r]]: bit-identical to the plain kernels on the gathered rows
+    a[a_rows] (same data, same MFMA order)."""
+    g = torch.Generator().manual_seed(sum(sizes))
+    T = 113
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16).to(cuda)
+    rows = torch.randint(0, T, (sum(sizes),), generator=g, dtype=torch.int32).to(cuda)
+    w = (torch.randn(len(sizes), N, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(cuda)
+    wu = (torch.randn(len(sizes), N, K, generator=g) / K ** 0.5).to(torch.bfloat16).to(cuda)
+    offs = inclusive(sizes, cuda)
+    xg = x[rows.long()].contiguous()
+    print("grouped rows sizes=%s N=%d K=%d" % (sizes, N, K), flush=True)
+    got = M.grouped_gemm(x, w, offs, a_rows=rows)
+    ref = M.grouped_gemm(xg, w, offs)
+    hg = M.grouped_swiglu(x, w, wu, offs, a_rows=rows)
+    hr = M.grouped_swiglu(xg, w, wu, offs)
+    torch.cuda.synchronize()
+    assert got.shape == (sum(sizes), N)
+    assert torch.equal(got, ref)
+    assert torch.equal(hg, hr)
