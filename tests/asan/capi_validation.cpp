@@ -46,6 +46,14 @@ int main() {
   EXPECT(moe_grouped_gemm(fake, fake, ip, 4, 64, 128, 256, nullptr, 3, fake, fake, 4096, nullptr), MOE_ERR_NULL_POINTER);
   EXPECT(moe_grouped_gemm(fake, fake, ip, 4, 64, 128, 256, nullptr, 0, fake, fake, 8, nullptr), MOE_ERR_WORKSPACE);
   EXPECT(moe_grouped_swiglu(fake, fake, nullptr, ip, 4, 64, 128, 256, nullptr, 0, fake, fake, 4096, nullptr), MOE_ERR_NULL_POINTER);
+  EXPECT(moe_grouped_gemm_rows(fake, nullptr, fake, ip, 4, 64, 128, 256, fake, fake, 4096, nullptr), MOE_ERR_NULL_POINTER);
+  EXPECT(moe_grouped_swiglu_rows(fake, ip, fake, fake, ip, 4, 64, 128, 200, fake, fake, 4096, nullptr), MOE_ERR_UNSUPPORTED);
+  const int8_t* q8 = (const int8_t*)fake;
+  EXPECT(moe_grouped_gemm_i8(q8, fp, nullptr, q8, fp, ip, 4, 64, 128, 192, nullptr, nullptr, 0, fake, fake, 4096, nullptr), MOE_ERR_UNSUPPORTED);
+  EXPECT(moe_grouped_swiglu_i8(q8, nullptr, nullptr, q8, fp, q8, fp, ip, 4, 64, 128, 256, nullptr, nullptr, 0, fake, fake, 4096, nullptr), MOE_ERR_NULL_POINTER);
+  EXPECT(moe_quant_rows_i8(fake, 4, 256, 64, 1.0f, 0, nullptr, (int8_t*)fake, fp, nullptr), MOE_ERR_INVALID_ARG);
+  EXPECT(moe_quant_rows_i8(fake, 6, 256, 16, 1.0f, 4, ip, (int8_t*)fake, fp, nullptr), MOE_ERR_INVALID_ARG);
+  EXPECT(moe_quant_rows_i8(nullptr, 0, 256, 0, 1.0f, 0, nullptr, nullptr, nullptr, nullptr), MOE_OK);
   if (moe_grouped_gemm_workspace_bytes(64) != 512) ++failures;
   if (moe_route_workspace_bytes(32768, 7168, 256, MOE_DTYPE_BF16) != (size_t)32768 * 2 * 256 * 4) ++failures;
   if (moe_permute_workspace_bytes(32768, 256, 8) != (size_t)256 * 1024 * 4 + 1024) ++failures;
