@@ -15,10 +15,12 @@
 // is sized by the bound sum ceil(m_g / BM) <= ceil(M / BM) + G; blocks past
 // the last tile return at once.
 //
-// Tiles: 256 rows x 256 weight rows, 64-wide K steps, staged in LDS by the
-// gfx950 global_load_lds DMA into a 2-stage ring with an XOR-swizzled 16-byte
-// chunk layout, v_mfma_f32_16x16x32_bf16 accumulators (bf16 A: 8 waves of
-// 64 x 128 with a software-pipelined K loop; fp8 A: 16 waves of 64 x 64).
+// Tiles: 256 rows x 256 weight rows (128 x 512 for groups of at most 320
+// rows on average), 128-byte K steps (64 bf16 or 128 int8 elements), staged
+// in LDS by the gfx950 global_load_lds DMA into a 2-stage ring with an
+// XOR-swizzled 16-byte chunk layout, v_mfma_f32_16x16x32_bf16 or
+// v_mfma_i32_16x16x64_i8 accumulators (bf16 / int8 A: 8 waves of 64 x 128
+// with a software-pipelined K loop; fp8 A: 16 waves of 64 x 64, plain loop).
 // Block ids are remapped so that each XCD runs a contiguous range of logical
 // tiles, and inside a group the tiles go in 4 x 8 (row x column) super-tiles:
 // the blocks running together on one XCD share A and weight slices in L2.
@@ -26,8 +28,8 @@
 // swiglu interleaves the two weights at 16-row granularity inside the B
 // tile (rows 16f..16f+15 come from wg for even f, from wu for odd f), so the
 // gate and up accumulators of the same output columns sit in one wave and
-// the epilogue forms h without an exchange.  A tile then covers 128 output
-// columns.
+// the epilogue forms h without an exchange.  A tile then covers half its
+// weight rows in output columns.
 //
 // Identity shortcut (the reference's ident_a / ident_m): a group whose row
 // count equals ident_m takes its A rows from ident_a (row i of the group =
@@ -36,7 +38,7 @@
 
 namespace moe {
 
-constexpr int kGgBN = 256;  // weight rows per tile (row tiles: 128 or 256, a template parameter)
+constexpr int kGgBN = 256;  // narrowest tile: weight rows per tile (tile shape: template parameters)
 
 // One workgroup of 1024 threads: inclusive scan of per-group tile counts.
 __global__ __launch_bounds__(1024) void gg_plan_kernel(const int* __restrict__ offs, int G, int M,
@@ -132,7 +134,8 @@ struct GgExtra {
   const float* w1;     // [G, N] per weight row of w1 (SwiGLU up)
 };
 
-template <bool SWIGLU, bool AFP8, int BK, int NS, int WM, int WN, bool PIPE, int BM, bool I8>
+template <bool SWIGLU, bool AFP8, int BK, int NS, int WM, int WN, bool PIPE, int BM, bool I8,
+          int BNT>
 __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
     const void* __restrict__ a_, const float* __restrict__ a_scales, const void* __restrict__ ident_,
     int ident_m, const void* __restrict__ w0_, const void* __restrict__ w1_,
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   // LDS rows: B (weights) BK*WEL bytes; A BK*2 bytes (bf16) or BK bytes (fp8,
   // int8).  bf16 steps are 64 wide, int8 steps 128 wide: 128-byte rows either
   // way.  A DMA wave instruction moves 1 KB = 1024 / row-bytes rows.
-  constexpr int BN = kGgBN;
+  constexpr int BN = BNT;  // weight rows per tile
   constexpr int WEL = I8 ? 1 : 2;  // bytes per weight element
   constexpr int ROWB = BK * WEL, CH = ROWB / 16, RPI = 1024 / ROWB;
   constexpr int AROWB = (AFP8 || I8) ? BK : BK * 2, ACH = AROWB / 16, ARPI = 1024 / AROWB;
@@ -164,9 +167,11 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   static_assert(!AFP8 || BK == 64, "fp8 A: one 128-wide scale block spans two K steps");
   static_assert(!AFP8 || (BM * ACH) % NT == 0, "fp8 A: whole 16-byte chunks per thread per K step");
   static_assert(!SWIGLU || FN % 2 == 0, "swiglu: gate/up fragment pairs inside one wave");
-  static_assert(!PIPE || (!AFP8 && ROWB == 128 && NS == 2 && WM == 4 && WN == 2 && BM == 256),
-                "pipelined loop: bf16 / int8 A, 256-row tiles, 2 stages of 128-byte rows, "
-                "8 waves of 64 x 128");
+  static_assert(!PIPE || (!AFP8 && ROWB == 128 && NS == 2 &&
+                          ((BM == 256 && BN == 256 && WM == 4 && WN == 2) ||
+                           (BM == 128 && BN == 512 && WM == 2 && WN == 4))),
+                "pipelined loop: bf16 / int8 A, 2 stages of 128-byte rows, 8 waves of 64 x 128: "
+                "256 x 256 or 128 x 512 tiles");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B + DQ_BYTES];
   char* const dq = lds + NS * STAGE_B;
   const char* a = (const char*)a_;
@@ -320,7 +325,9 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
                                        0, 0);
     };
     constexpr int kReads = FM + FN;
-    static_assert(2 * kReads <= FM * FN && 4 * PER_WAVE <= FM * FN,
+    // DMA instruction q follows MFMA q * kDs + kDs / 2
+    constexpr int kDs = FM * FN >= 4 * PER_WAVE ? 4 : 2;
+    static_assert(2 * kReads <= FM * FN && kDs * PER_WAVE <= FM * FN,
                   "the reads and the DMA fit between the MFMAs of a half step");
     // MFMAs on (av, bv); reads into (ra, rb) from (rab, rbb) when rd; DMA of
     // stage dkt into buffer dst when dkt >= 0
@@ -334,7 +341,7 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
           if (r < FM) read_one(ra[r], rab + r * 2048);
           else read_one(rb[r - FM], rbb + (r - FM) * 2048);
         }
-        if ((t & 3) == 2 && (t >> 2) < PER_WAVE && dkt >= 0) dma_one(t >> 2, dkt, dst);
+        if (t % kDs == kDs / 2 && t / kDs < PER_WAVE && dkt >= 0) dma_one(t / kDs, dkt, dst);
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -530,8 +537,13 @@ int grouped_gemm_n_tiles(int N, bool swiglu) {
   const int per = swiglu ? kGgBN / 2 : kGgBN;
   return (N + per - 1) / per;
 }
+template <int BNT>
+static int n_tiles_of(int N, bool swiglu) {
+  const int per = swiglu ? BNT / 2 : BNT;
+  return (N + per - 1) / per;
+}
 
-template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS, bool I8 = false>
+template <bool AFP8, int WM, int WN, bool PIPE, int BM, int NS, bool I8 = false, int BNT = 256>
 static hipError_t launch_gg(const void* a, const float* a_scales, const void* ident_a, int ident_m,
                             const void* w0, const void* w1, const int32_t* offs, int G, int M, int N,
                             int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s,
@@ -541,17 +553,17 @@ static hipError_t launch_gg(const void* a, const float* a_scales, const void* id
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (M == 0 || N == 0 || G == 0) return hipSuccess;
-  const int n_tiles = grouped_gemm_n_tiles(N, swiglu);
+  const int n_tiles = n_tiles_of<BNT>(N, swiglu);
   const long long m_bound = ((long long)M + BM - 1) / BM + G;
   long long blocks = m_bound * n_tiles;
   blocks = (blocks + 7) / 8 * 8;
   const dim3 grid((unsigned)blocks), blk(64 * WM * WN);
   if (swiglu)
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, BK, NS, WM, WN, PIPE, BM, I8>), grid, blk,
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, AFP8, BK, NS, WM, WN, PIPE, BM, I8, BNT>), grid, blk,
                        0, s, a, a_scales, ident_a, ident_m, w0, w1, offs, tile_start, G, M, N, K,
                        n_tiles, (unsigned short*)out, i8s);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, BK, NS, WM, WN, PIPE, BM, I8>), grid, blk,
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, AFP8, BK, NS, WM, WN, PIPE, BM, I8, BNT>), grid, blk,
                        0, s, a, a_scales, ident_a, ident_m, w0, w0, offs, tile_start, G, M, N, K,
                        n_tiles, (unsigned short*)out, i8s);
   return hipGetLastError();
@@ -571,14 +583,19 @@ hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const int32
   if (a_scales)
     return launch_gg<true, 4, 4, false, 256, 2>(a, a_scales, ident_a, ident_m, w0, w1, offs, G, M,
                                                 N, K, swiglu, out, tile_start, s);
-  // bf16 A with small groups (<= 320 rows on average, e.g. T = 1571-2048
-  // routed top-8 over 64 experts): the weights stream from HBM with little
-  // reuse, so 128-row tiles with a 3-stage ring (2 stages in flight) win --
-  // measured 7-16% faster at T = 1571, 10% slower at T = 8192.
+  // bf16 A with at most 320 rows per group on average (e.g. T = 1571-2048
+  // routed top-8 over 64 experts, or 8 groups of T rows): 128 x 512 tiles.
+  // Against 256 x 256 they pad a group's last row tile less and leave less of
+  // a tail round; against 128 x 256 they move 40 instead of 48 bytes per
+  // K step per 1024 MFMA cycles.  The pipelined loop with 8 waves of 64 x
+  // 128, as below.  Measured at T = 1571 / 2048: int8 run() 2.82 / 3.27 ms
+  // against 2.93 / 3.44 with plain-loop 128 x 256 tiles; at T = 8192 they
+  // are 5-10% slower than 256 x 256.
   if ((long long)M <= 320ll * G)
-    return launch_gg<false, 2, 8, false, 128, 3>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M,
-                                                 N, K, swiglu, out, tile_start, s, ex);
-  // bf16 A, larger groups: 256-row tiles, 8 waves of 64 x 128 accumulators,
+    return launch_gg<false, 2, 4, true, 128, 2, false, 512>(a, nullptr, ident_a, ident_m, w0, w1,
+                                                            offs, G, M, N, K, swiglu, out,
+                                                            tile_start, s, ex);
+  // bf16 A, larger groups: 256 x 256 tiles, 8 waves of 64 x 128 accumulators,
   // the software-pipelined K loop.
   return launch_gg<false, 4, 2, true, 256, 2>(a, nullptr, ident_a, ident_m, w0, w1, offs, G, M, N,
                                               K, swiglu, out, tile_start, s, ex);
@@ -593,8 +610,9 @@ hipError_t launch_grouped_gemm_i8(const void* a, const float* a_rs, const int32_
                                   bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
   const GgExtra sc{a_rs, a_rs_idx, ident_rs, w0s, swiglu ? w1s : w0s};
   if ((long long)M <= 320ll * G)
-    return launch_gg<false, 2, 8, false, 128, 3, true>(a, nullptr, ident_a, ident_m, w0, w1, offs,
-                                                       G, M, N, K, swiglu, out, tile_start, s, sc);
+    return launch_gg<false, 2, 4, true, 128, 2, true, 512>(a, nullptr, ident_a, ident_m, w0, w1,
+                                                           offs, G, M, N, K, swiglu, out,
+                                                           tile_start, s, sc);
   return launch_gg<false, 4, 2, true, 256, 2, true>(a, nullptr, ident_a, ident_m, w0, w1, offs, G,
                                                     M, N, K, swiglu, out, tile_start, s, sc);
 }
