@@ -106,8 +106,11 @@ def cpu_baseline(c, sample_T):
 LAYER_MIX = {1571: 1, 2048: 1, 4096: 3, 4904: 1, 8192: 3}  # kernel.cu:133-136
 
 
-def layer_bench(Ts, steps, warmup, dispatch="bf16", experts="bf16"):
-    """run() latency per T (HIP events around each call, median of `steps`)."""
+def layer_bench(Ts, steps, warmup, dispatch="bf16", experts="bf16", cold=True):
+    """run() latency per T (HIP events around each call, median of `steps`).
+    cold: before each timed call a 1 GiB buffer is rewritten, evicting L2 and
+    the 256 MB MALL, as the reference's harness times each call with a cold
+    L2 (kernel.cu:146-151)."""
     dev = torch.device("cuda:0")
     H, E, Ni, SNi = 8192, 64, 3584, 7168
     g = torch.Generator(device=dev).manual_seed(0)
@@ -120,6 +123,7 @@ def layer_bench(Ts, steps, warmup, dispatch="bf16", experts="bf16"):
     sg = (r(SNi, H) / H ** 0.5).to(torch.bfloat16)
     su = (r(SNi, H) / H ** 0.5).to(torch.bfloat16)
     sd = (r(H, SNi) / SNi ** 0.5).to(torch.bfloat16)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev) if cold else None
     ms = {}
     for T in Ts:
         hs = r(1, T, H).to(torch.bfloat16)
@@ -130,6 +134,8 @@ def layer_bench(Ts, steps, warmup, dispatch="bf16", experts="bf16"):
         torch.cuda.synchronize()
         ts = []
         for _ in range(steps):
+            if flush is not None:
+                flush.fill_(1)
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
             a.record()
@@ -149,6 +155,7 @@ def layer_bench(Ts, steps, warmup, dispatch="bf16", experts="bf16"):
         "config": {"workload": "kernel.cu run(): NE=64 H=8192 Ni=3584 SNi=7168 top-8; value = "
                                "sum over T of mix weight x latency",
                    "dispatch": dispatch, "experts": experts,
+                   "cache": "cold (1 GiB rewritten before each timed call)" if cold else "warm",
                    "mix": {str(T): LAYER_MIX.get(T, 1) for T in Ts}},
         "per_T_ms": {str(T): round(v, 4) for T, v in ms.items()},
         "reference_b200_mix_sum_ms": 35.92,
@@ -171,6 +178,8 @@ def main():
                     help="time run() at the reference's workload T values (default: its mix)")
     ap.add_argument("--layer-fp8", action="store_true",
                     help="with --layer: run(..., dispatch='fp8')")
+    ap.add_argument("--layer-warm", action="store_true",
+                    help="with --layer: no cache flush between the timed calls")
     ap.add_argument("--layer-int8", action="store_true",
                     help="with --layer: run(..., experts='int8'), the reference's expert precision")
     args = ap.parse_args()
@@ -181,7 +190,8 @@ def main():
 
     if args.layer is not None:
         layer_bench(args.layer or sorted(LAYER_MIX), max(args.steps // 2, 5), 2,
-                    "fp8" if args.layer_fp8 else "bf16", "int8" if args.layer_int8 else "bf16")
+                    "fp8" if args.layer_fp8 else "bf16", "int8" if args.layer_int8 else "bf16",
+                    cold=not args.layer_warm)
         return
 
     c = CONFIGS[args.config]
