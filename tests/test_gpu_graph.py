@@ -66,3 +66,34 @@ def test_two_streams_concurrently(cuda):
     for p, wnt in zip(plans, want):
         for n, v in wnt.items():
             assert torch.equal(getattr(p, n), v), n
+
+
+@pytest.mark.parametrize("experts", ["bf16", "int8"])
+def test_run_graph_capture_replays(cuda, experts):
+    """The whole reference entry point run() -- routing, index-only permute,
+    expert and shared-expert GEMMs (bf16 or int8 with its quantisers),
+    combine -- captured in one HIP graph: every stage is stream-ordered, with
+    no host synchronisation and no memset.  Each replay equals the eager call
+    bit for bit, with eager calls (which reuse the same kernels and scribble
+    over device memory) between the replays."""
+    from test_gpu_run import make
+    args = [a.to(cuda) for a in make(seed=9)]
+    norm_min = 1e-6
+    out_e, logits_e = M.run(*args, norm_min, experts=experts)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        M.run(*args, norm_min, experts=experts)        # warm up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out_g, logits_g = M.run(*args, norm_min, experts=experts)
+    for rep in range(3):
+        M.run(*args, norm_min, experts=experts)        # eager work in between
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(logits_g, logits_e), rep
+        assert torch.equal(out_g, out_e), rep
