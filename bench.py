@@ -88,17 +88,27 @@ def cpu_baseline(c, sample_T):
     b = None if bias is None else bias.numpy()
 
     def once():
-        O.route_dispatch_combine(x, w, b, y, c.k, cfg, fp8=c.fp8)
+        """The oracle's route_dispatch_combine, stage by stage: seconds per stage."""
+        t = [time.perf_counter()]
+        r = O.route(x, w, b, c.k, cfg)
+        t.append(time.perf_counter())
+        row_token, pair_row = O.permutation(r["ids"])
+        if c.fp8:
+            O.permute_fp8(x, row_token)
+        else:
+            O.gather_rows(x, row_token)
+        t.append(time.perf_counter())
+        O.combine(y, pair_row, r["weights"])
+        t.append(time.perf_counter())
+        return [t[i + 1] - t[i] for i in range(3)]
 
     once()
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        once()
-        ts.append(time.perf_counter() - t0)
-    med = statistics.median(ts)
+    runs = [once() for _ in range(3)]
+    med = statistics.median(sum(r) for r in runs)
+    stages = {n: round(statistics.median(r[i] for r in runs), 4)
+              for i, n in enumerate(("route", "permute", "combine"))}
     return {"value": sample_T / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", "stages_s": stages,
             "sample": "%d tokens of %s (T,H,E,k = %d,%d,%d,%d), oracle route+permute+combine, "
                       "median of 3 = %.3f s" % (sample_T, c.name, sample_T, c.H, c.E, c.k, med)}
 
@@ -244,6 +254,21 @@ def main():
         st["permute_index"].append(e[3].elapsed_time(e[4]) * 1e3)
         st["topk"].append(e[4].elapsed_time(e[5]) * 1e3)
     us = {k2: statistics.mean(v) for k2, v in st.items()}
+
+    # ---- cold-cache step: 20 single steps, each after a 1 GiB rewrite that
+    # evicts L2 and the MALL (reported beside `value`, which is the K-step rate)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    cold = []
+    for _ in range(20):
+        flush.fill_(1)
+        e0, e1 = ev(), ev()
+        e0.record()
+        plan.step(x, w, bias, y)
+        e1.record()
+        e1.synchronize()
+        cold.append(e0.elapsed_time(e1))
+    del flush
+    cold_ms = statistics.median(cold)
     us["gather"] = us["permute"] - us["permute_index"]
     us["router_gemm"] = max(us["route"] - us["topk"], 1e-3)
 
@@ -291,6 +316,8 @@ def main():
             "gather": round(ab["gather"] / (us["gather"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "combine": round(ab["combine"] / (us["combine"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
         "router_gemm": gemm,
+        "cold_step": {"ms": round(cold_ms, 4), "tokens_per_s": round(c.T / (cold_ms * 1e-3), 1),
+                      "note": "median of 20 single steps, each after a 1 GiB rewrite (L2 + MALL)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
