@@ -75,13 +75,14 @@ def measured_traffic(config):
     return out
 
 
-def cpu_baseline(c, sample_T):
+def cpu_baseline(c, sample_T, threads=0):
     """The CPU oracle (oracle/moe_oracle.py) on `sample_T` tokens of the same
     workload: router GEMM (torch fp32), scoring/top-k, permutation, gather /
     fp8 quantisation and combine.  1 warm-up + median of 3."""
     from oracle import moe_oracle as O
-    ncores = len(os.sched_getaffinity(0))
+    ncores = threads or len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
+    sample_T = min(sample_T, c.T)
     x, w, bias, y = M.make_inputs(c, T=sample_T, seed=0)
     cfg = O.RouteCfg(c.cfg.scoring, c.cfg.renormalize, c.cfg.n_group, c.cfg.topk_group,
                      c.cfg.route_scale, c.cfg.norm_min)
@@ -95,10 +96,11 @@ def cpu_baseline(c, sample_T):
         row_token, pair_row = O.permutation(r["ids"])
         if c.fp8:
             O.permute_fp8(x, row_token)
+            xg = None
         else:
-            O.gather_rows(x, row_token)
+            xg = O.gather_rows(x, row_token)
         t.append(time.perf_counter())
-        O.combine(y, pair_row, r["weights"])
+        O.combine(xg if y is None else y, pair_row, r["weights"])  # y None: identity experts
         t.append(time.perf_counter())
         return [t[i + 1] - t[i] for i in range(3)]
 
@@ -181,6 +183,8 @@ def main():
     ap.add_argument("--config", default="C4")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=16384)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads for the CPU baseline (0: every core of this process)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one plain 1 GiB device copy (untimed), the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
@@ -294,7 +298,7 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(c, args.cpu_tokens)
+        cpu = cpu_baseline(c, args.cpu_tokens, args.cpu_threads)
 
     tok_s = c.T / (ms_per_step * 1e-3)
     line = {

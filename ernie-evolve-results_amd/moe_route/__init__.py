@@ -617,12 +617,16 @@ class MoePlan:
                                  _stream(x)))
 
     def combine(self, y, shared=None):
+        if y is None:  # identity experts: combine the gathered rows
+            y = self.xg
         _check(lib().moe_combine(_ptr(y), _dtype_code(y.dtype), _ptr(self.pair_row),
                                  _ptr(self.topk_w), _ptr(shared), self.T, self.H, self.k,
                                  _ptr(self.out), _stream(y)))
 
     def step(self, x, w, bias, y):
-        """route -> permute -> combine for one batch."""
+        """route -> permute -> combine for one batch.  y None: identity experts
+        (the C1 configuration), i.e. the gathered rows are combined, which
+        returns x when the weights sum to 1."""
         self.route(x, w, bias)
         self.permute(x)
         self.combine(y)
