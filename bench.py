@@ -46,11 +46,12 @@ def algorithmic_bytes(c):
     by the permute; each routed row written once and read once)."""
     T, H, E, k = c.T, c.H, c.E, c.k
     xb = 2
+    wb = 4 if c.x_dtype == torch.float32 else 2  # an fp32 router weight is read whole
     db = 1 if c.fp8 else 2
-    route = T * H * xb + E * H * 2 + T * E * 4 + T * k * 8
+    route = T * H * xb + E * H * wb + T * E * 4 + T * k * 8
     gather = T * H * xb + T * k * H * db + (T * k * (H // 128) * 4 if c.fp8 else 0) + T * k * 8
     combine = T * k * H * 2 + T * H * 2 + T * k * 8
-    return dict(route=route, gather=gather, combine=combine, router_gemm=T * H * xb + E * H * 2
+    return dict(route=route, gather=gather, combine=combine, router_gemm=T * H * xb + E * H * wb
                 + T * E * 4)
 
 
@@ -211,7 +212,11 @@ def main():
     c = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
-    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, dev, fp8=c.fp8)
+    # The router takes bf16 hidden states (K:4327-4339); an fp32 config (C1)
+    # hands the GPU path bf16(x), cast once here, and keeps its fp32 router
+    # weight, which moe_route splits into bf16 hi/lo on the device.
+    x = x.to(torch.bfloat16)
+    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, dev, fp8=c.fp8, w_dtype=w.dtype)
     torch.cuda.synchronize()
 
     for _ in range(args.warmup):
@@ -309,7 +314,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded randn inputs generated on the GPU)",
         "config": {"workload": "%s route+dispatch+combine: %s" % (c.name, c.description),
-                   "T": c.T, "H": c.H, "E": c.E, "k": c.k, "fp8_dispatch": c.fp8},
+                   "T": c.T, "H": c.H, "E": c.E, "k": c.k, "fp8_dispatch": c.fp8,
+                   "x": "bf16", "router_weight": str(w.dtype).replace("torch.", "")},
         "roofline": roofline,
         "e2e_hbm": {"algorithmic_bytes": total_bytes, "achieved": round(e2e_gbs, 1),
                     "unit": "GB/s", "frac": round(e2e_gbs / HBM_PEAK_GBS, 4)},
