@@ -129,6 +129,33 @@ def _dev(t, name):
     return t
 
 
+def _want(t, name, dtypes, shape=None):
+    """Check dtype and shape; the caller then checks the device of every
+    argument with _devs.  The C ABI takes bare pointers: a wrong dtype or
+    shape here would be read as another layout, or written past the end of a
+    buffer."""
+    if not isinstance(t, torch.Tensor):
+        raise RuntimeError("%s must be a tensor" % name)
+    if t.dtype not in dtypes:
+        raise RuntimeError("%s must be %s, got %s" % (
+            name, " or ".join(str(d).replace("torch.", "") for d in dtypes),
+            str(t.dtype).replace("torch.", "")))
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise RuntimeError("%s must have shape %s, got %s" % (name, tuple(shape), tuple(t.shape)))
+    return t
+
+
+def _devs(**named):
+    """_dev on every tensor argument that is not None."""
+    for name, t in named.items():
+        if t is not None:
+            _dev(t, name)
+
+
+_BF16, _F32, _I32 = (torch.bfloat16,), (torch.float32,), (torch.int32,)
+_BF16_F32 = (torch.bfloat16, torch.float32)
+
+
 def _stream(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
@@ -164,10 +191,11 @@ def router_gemm(x, w):
 def topk(logits, bias, k, cfg: RouteCfg):
     """Scoring + top-k + histogram on fp32 logits (K:1829-1920).
     Returns (topk_ids int32 [T,k], topk_w fp32 [T,k], counts int32 [E])."""
-    _dev(logits, "logits")
+    _want(logits, "logits", _F32)
     T, E = logits.shape
     if bias is not None:
-        _dev(bias, "bias")
+        _want(bias, "bias", _F32, (E,))
+    _devs(logits=logits, bias=bias)
     ids = torch.empty(T, k, dtype=torch.int32, device=logits.device)
     wts = torch.empty(T, k, dtype=torch.float32, device=logits.device)
     counts = torch.empty(E, dtype=torch.int32, device=logits.device)
@@ -181,12 +209,14 @@ def route(x, w, bias, k, cfg: RouteCfg):
     """Router GEMM + scoring + top-k + histogram.  w bf16 [E,H], or fp32 [E,H]
     (hi/lo split on the device, K:1786-1824).
     Returns (logits fp32 [T,E], topk_ids, topk_w, counts)."""
-    _dev(x, "x"), _dev(w, "w")
+    _want(x, "x", _BF16)  # the router reads bf16 hidden states (K:4327-4339)
     T, H = x.shape
     E = w.shape[0]
+    _want(w, "w", _BF16_F32, (E, H))
     wd = _dtype_code(w.dtype)
     if bias is not None:
-        _dev(bias, "bias")
+        _want(bias, "bias", _F32, (E,))
+    _devs(x=x, w=w, bias=bias)
     dev = x.device
     logits = torch.empty(T, E, dtype=torch.float32, device=dev)
     ids = torch.empty(T, k, dtype=torch.int32, device=dev)
@@ -216,9 +246,11 @@ def permute(x, topk_ids, E, fp8=False, index_only=False):
 
     Returns dict(xg, scales, row_token, pair_row, offsets, counts); xg is
     x.dtype rows (or uint8 e4m3fn bytes when fp8) in expert-contiguous order."""
-    _dev(x, "x"), _dev(topk_ids, "topk_ids")
+    _want(x, "x", _BF16_F32)
     T, H = x.shape
     k = topk_ids.shape[1]
+    _want(topk_ids, "topk_ids", _I32, (T, k))
+    _devs(x=x, topk_ids=topk_ids)
     dev = x.device
     xd = _dtype_code(x.dtype)
     od = DTYPE_FP8E4M3FN if fp8 else xd
@@ -247,13 +279,21 @@ def permute(x, topk_ids, E, fp8=False, index_only=False):
 def combine(y, pair_row, topk_w, shared=None, out=None):
     """out[t] = shared[t] + sum_j w[t,j] * y[pair_row[t,j]], fp32 accumulate
     (K:2365-2428)."""
-    _dev(y, "y"), _dev(pair_row, "pair_row"), _dev(topk_w, "topk_w")
+    _want(y, "y", _BF16_F32)
+    _want(topk_w, "topk_w", _F32)
     T, k = topk_w.shape
     H = y.shape[1]
+    _want(pair_row, "pair_row", _I32)
+    if pair_row.numel() != T * k:  # [T, k] or moe_permute's flat [T * k]
+        raise RuntimeError("pair_row must hold T * k = %d entries, got %d" % (T * k,
+                                                                            pair_row.numel()))
     if shared is not None:
-        _dev(shared, "shared")
+        _want(shared, "shared", (y.dtype,), (T, H))
     if out is None:
         out = torch.empty(T, H, dtype=y.dtype, device=y.device)
+    else:
+        _want(out, "out", (y.dtype,), (T, H))
+    _devs(y=y, topk_w=topk_w, pair_row=pair_row, shared=shared, out=out)
     _check(lib().moe_combine(_ptr(y), _dtype_code(y.dtype), _ptr(pair_row), _ptr(topk_w),
                              _ptr(shared), T, H, k, _ptr(out), _stream(y)))
     return out
@@ -581,7 +621,8 @@ class MoePlan:
         else:
             self.xg = torch.empty(ns, H, dtype=x_dtype, device=dev)
             self.scales = None
-        self.out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        self.x_dtype, self.w_dtype = x_dtype, w_dtype
+        self.out = torch.empty(T, H, dtype=x_dtype, device=dev)  # combine writes y's dtype
         self.nws_route = L.moe_route_workspace_bytes(T, H, E, self.wd)
         self.ws_route = torch.empty(max(self.nws_route, 256), dtype=torch.uint8, device=dev)
         self.nws_perm = L.moe_permute_workspace_bytes(T, E, k)
@@ -591,6 +632,11 @@ class MoePlan:
         """Router GEMM + scoring + top-k.  The per-expert counts are also
         produced by ``permute``; ``counts=True`` additionally fills
         ``route_counts`` from the scoring kernel's histogram."""
+        _want(x, "x", _BF16, (self.T, self.H))
+        _want(w, "w", (self.w_dtype,), (self.E, self.H))
+        if bias is not None:
+            _want(bias, "bias", _F32, (self.E,))
+        _devs(x=x, w=w, bias=bias)
         _check(lib().moe_route(_ptr(x), _ptr(w), self.wd, _ptr(bias), self.T, self.H, self.E,
                                self.k, ctypes.byref(self.cfg), _ptr(self.logits),
                                _ptr(self.topk_ids), _ptr(self.topk_w),
@@ -598,6 +644,9 @@ class MoePlan:
                                _ptr(self.ws_route), self.nws_route, _stream(x)))
 
     def router_gemm(self, x, w):
+        _want(x, "x", _BF16, (self.T, self.H))
+        _want(w, "w", _BF16, (self.E, self.H))
+        _devs(x=x, w=w)
         _check(lib().moe_router_gemm(_ptr(x), _ptr(w), self.T, self.H, self.E, _ptr(self.logits),
                                      _stream(x)))
 
@@ -608,6 +657,7 @@ class MoePlan:
                               _stream(self.logits)))
 
     def permute(self, x, index_only=False):
+        _devs(x=_want(x, "x", (self.x_dtype,), (self.T, self.H)))
         od = DTYPE_FP8E4M3FN if self.fp8 else self.xd
         _check(lib().moe_permute(_ptr(x), self.xd, _ptr(self.topk_ids), self.T, self.H, self.E,
                                  self.k, od, None if index_only else _ptr(self.xg),
@@ -618,7 +668,14 @@ class MoePlan:
 
     def combine(self, y, shared=None):
         if y is None:  # identity experts: combine the gathered rows
+            if self.fp8:
+                raise RuntimeError("identity experts need the bf16 / fp32 permute (fp8 rows "
+                                   "are not a combine input)")
             y = self.xg
+        _want(y, "y", (self.out.dtype,), (self.T * self.k, self.H))
+        if shared is not None:
+            _want(shared, "shared", (self.out.dtype,), (self.T, self.H))
+        _devs(y=y, shared=shared)
         _check(lib().moe_combine(_ptr(y), _dtype_code(y.dtype), _ptr(self.pair_row),
                                  _ptr(self.topk_w), _ptr(shared), self.T, self.H, self.k,
                                  _ptr(self.out), _stream(y)))

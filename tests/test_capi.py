@@ -198,6 +198,52 @@ def test_python_layer_refuses_cpu_tensors():
         M.quant_rows_i8(x)
 
 
+def test_python_layer_checks_dtype_and_shape_first():
+    """A wrong dtype or shape is refused before the bare pointer reaches the C
+    ABI (it would be read as another layout, or written past a buffer)."""
+    xf = torch.zeros(4, 64)
+    xb = xf.to(torch.bfloat16)
+    w = torch.zeros(8, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="x must be bfloat16, got float32"):
+        M.route(xf, w, None, 2, M.RouteCfg())
+    with pytest.raises(RuntimeError, match=r"w must have shape \(8, 64\)"):
+        M.route(xb, w[:, :32], None, 2, M.RouteCfg())
+    with pytest.raises(RuntimeError, match="bias must be float32"):
+        M.route(xb, w, torch.zeros(8, dtype=torch.bfloat16), 2, M.RouteCfg())
+    with pytest.raises(RuntimeError, match="topk_ids must be int32"):
+        M.permute(xb, torch.zeros(4, 2, dtype=torch.int64), 8)
+    with pytest.raises(RuntimeError, match="pair_row must hold T"):
+        M.combine(xb.repeat(2, 1), torch.zeros(7, dtype=torch.int32), torch.zeros(4, 2))
+    with pytest.raises(RuntimeError, match="out must be bfloat16"):
+        M.combine(xb.repeat(2, 1), torch.zeros(4, 2, dtype=torch.int32), torch.zeros(4, 2),
+                  out=torch.zeros(4, 64))
+    with pytest.raises(RuntimeError, match="logits must be float32"):
+        M.topk(xb, None, 2, M.RouteCfg())
+
+
+def test_plan_checks_inputs_against_its_shape():
+    """MoePlan (buffers allocated for one shape) refuses inputs of another
+    dtype or shape; its combine output takes the rows' dtype."""
+    plan = M.MoePlan(4, 64, 8, 2, M.RouteCfg(), "cpu", x_dtype=torch.float32,
+                     w_dtype=torch.float32)
+    assert plan.out.dtype == torch.float32 and plan.xg.dtype == torch.float32
+    xf = torch.zeros(4, 64)
+    wf = torch.zeros(8, 64)
+    with pytest.raises(RuntimeError, match="x must be bfloat16, got float32"):
+        plan.route(xf, wf, None)  # the router reads bf16 hidden states
+    with pytest.raises(RuntimeError, match="w must be float32"):
+        plan.route(xf.to(torch.bfloat16), wf.to(torch.bfloat16), None)
+    with pytest.raises(RuntimeError, match=r"x must have shape \(4, 64\)"):
+        plan.permute(torch.zeros(5, 64))
+    with pytest.raises(RuntimeError, match="y must be float32"):
+        plan.combine(torch.zeros(8, 64, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        plan.combine(None)  # identity experts: the plan's own rows pass the checks
+    p8 = M.MoePlan(4, 128, 8, 2, M.RouteCfg(), "cpu", fp8=True)
+    with pytest.raises(RuntimeError, match="identity experts"):
+        p8.combine(None)
+
+
 def test_run_rejects_bad_options():
     """run()'s keyword options are checked before any device work."""
     hs = torch.zeros(1, 4, 64, dtype=torch.bfloat16)
