@@ -5,7 +5,9 @@
 // times.  Here the walk is over TOKENS: each x row is read from HBM once and
 // written to its k rows (pair_row[t*k + j]), which is the algorithmic minimum
 // T*H + T*k*H bytes.  Every thread moves one 16-byte vector, so a wavefront
-// reads 1 KB of one token row and writes k 1 KB runs.
+// reads 1 KB of one token row and writes k 1 KB runs.  x is loaded with
+// ordinary (temporal) loads, which hit the part of x the router GEMM left in
+// the memory-side cache (MALL); the k rows are written non-temporal.
 //
 // fp8 variant (the reference has no routed fp8 permute): a 16-lane group owns
 // one 1x128 block of a token row (8 bf16 per lane), reduces |x| max over the
@@ -24,7 +26,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
   for (int i = blockIdx.x * 256 + threadIdx.x; i < total; i += gridDim.x * 256) {
     const int t = i / nvec;
     const int v = i - t * nvec;
-    const u32x4 val = ld_nt(x + i);
+    const u32x4 val = x[i];
     const int* pr = pair_row + (long long)t * k;
     // all k row indices first (one wait), then the k stores
     int r[K > 0 ? K : 8];
@@ -80,7 +82,7 @@ __global__ __launch_bounds__(256) void gather_fp8_kernel(const u32x4* __restrict
   for (int g = (blockIdx.x * 256 + threadIdx.x) >> 4; g < ngroups; g += gridDim.x * 16) {
     const int t = g / nb;
     const int blk = g - t * nb;
-    const u32x4 raw = ld_nt(x + ((long long)t * H + blk * 128) / 8 + lane16);
+    const u32x4 raw = x[((long long)t * H + blk * 128) / 8 + lane16];
     float f[8];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {

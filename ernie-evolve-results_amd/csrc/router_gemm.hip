@@ -17,7 +17,12 @@
 // scoring kernel adds them in a fixed order (deterministic, no atomics).
 // 16 waves (4 per SIMD, 64x64 accumulator tiles) hide the DMA latency better
 // than 8 waves with 128x64 tiles (measured 122 vs 141 us at T = 32768).
-// x is loaded with the non-temporal bit: it streams through once.
+// x is loaded with ordinary (temporal) loads although the GEMM reads it once:
+// the part of x still held in the 256 MB memory-side cache (MALL) when the
+// permute reads x again is not fetched from HBM a second time.  Measured on
+// the C4 step: the GEMM is ~30 us slower than with non-temporal x loads, the
+// gather and the combine after it ~15 and ~55 us faster (1745 vs 1791 us per
+// step, outputs bit-identical).
 //
 // Smaller N use smaller row tiles (and split-K when even those leave the
 // chip idle): there the router weight is small and the GEMM is an x stream.
@@ -69,7 +74,7 @@ __global__ __launch_bounds__(64 * WM * WN) void router_gemm_dma_kernel(
   static_assert(FM >= 1 && FN >= 1, "wave tile below one MFMA tile");
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE_B];
 
-  // wave index as a scalar: the A/B choice of each DMA below is a uniform branch
+  // wave index as a scalar: the x / weight role of each DMA below is a uniform branch
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const long long m0 = (long long)blockIdx.x * BM;
@@ -102,10 +107,8 @@ __global__ __launch_bounds__(64 * WM * WN) void router_gemm_dma_kernel(
     for (int q = 0; q < PER_WAVE; ++q) {
       auto* dst = (__attribute__((address_space(3))) void*)(lds + st * STAGE_B +
                                                             (wave * PER_WAVE + q) * 1024);
-      if (wave * PER_WAVE + q < A_INST)  // x: streamed once, non-temporal
-        __builtin_amdgcn_global_load_lds((const void*)(src[q] + kt * BK), dst, 16, 0, 2);
-      else
-        __builtin_amdgcn_global_load_lds((const void*)(src[q] + kt * BK), dst, 16, 0, 0);
+      // x and the weight alike: temporal (x is read again by the permute)
+      __builtin_amdgcn_global_load_lds((const void*)(src[q] + kt * BK), dst, 16, 0, 0);
     }
   };
 
