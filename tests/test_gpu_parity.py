@@ -282,6 +282,52 @@ def test_permute_invalid_ids_are_dropped(cuda):
     assert to_np(p["offsets"])[-1] == 6
 
 
+@pytest.mark.parametrize("T,k,E,dist", [
+    (8192, 2, 8, "uniform"),      # C2: 16384 pairs
+    (8193, 2, 8, "uniform"),      # a last block of 2 pairs
+    (8192, 8, 64, "collapsed"),   # every token on the same 8 experts (run()'s harness routing)
+    (1571, 8, 64, "uniform"),
+    (3000, 8, 65, "uniform"),
+    (2000, 4, 1, "uniform"),      # one expert
+    (7, 3, 5, "uniform"),
+])
+def test_dispatch_index_paths(cuda, T, k, E, dist):
+    """The index kernels give the oracle's stable order on uniform, collapsed
+    and single-expert routing, with partial last blocks."""
+    g = torch.Generator().manual_seed(T * 131 + E)
+    if dist == "collapsed":
+        ids = torch.argsort(torch.rand(E, generator=g))[:k].int().repeat(T, 1)
+    else:
+        ids = torch.randint(0, E, (T, k), generator=g, dtype=torch.int32)
+    x = torch.empty(T, 64, dtype=torch.bfloat16, device=cuda)
+    print("dispatch index T=%d k=%d E=%d %s" % (T, k, E, dist), flush=True)
+    p = M.permute(x, ids.to(cuda), E, index_only=True)
+    torch.cuda.synchronize()
+    check_permutation(p, ids.numpy(), E)
+
+
+@pytest.mark.parametrize("T,E", [(5000, 8), (100000, 8), (3000, 64)])
+def test_dispatch_index_drops_invalid_ids(cuda, T, E):
+    """Out-of-range ids get pair_row -1 and no row; the valid pairs keep the
+    stable order among themselves."""
+    g = torch.Generator().manual_seed(T + E)
+    k = 2
+    ids = torch.randint(-2, E + 2, (T, k), generator=g, dtype=torch.int32)
+    x = torch.empty(T, 64, dtype=torch.bfloat16, device=cuda)
+    p = M.permute(x, ids.to(cuda), E, index_only=True)
+    torch.cuda.synchronize()
+    flat = ids.numpy().ravel()
+    ok = (flat >= 0) & (flat < E)
+    order = np.flatnonzero(ok)[np.argsort(flat[ok], kind="stable")]
+    want_pr = np.full(flat.size, -1, dtype=np.int32)
+    want_pr[order] = np.arange(order.size, dtype=np.int32)
+    assert np.array_equal(to_np(p["pair_row"]), want_pr)
+    assert np.array_equal(to_np(p["row_token"])[:order.size], (order // k).astype(np.int32))
+    c = np.bincount(flat[ok], minlength=E)
+    assert np.array_equal(to_np(p["counts"]), c)
+    assert np.array_equal(to_np(p["offsets"]), np.concatenate([[0], np.cumsum(c)]))
+
+
 def test_permute_empty(cuda):
     x = torch.empty(0, 64, dtype=torch.bfloat16, device=cuda)
     ids = torch.empty(0, 2, dtype=torch.int32, device=cuda)
