@@ -15,7 +15,7 @@
 // is sized by the bound sum ceil(m_g / BM) <= ceil(M / BM) + G; blocks past
 // the last tile return at once.
 //
-// Tiles: 256 rows x 256 weight rows (128 x 512 for groups of at most 320
+// Tiles: 256 rows x 256 weight rows (128 x 512 for groups of at most 128
 // rows on average), 128-byte K steps (64 bf16 or 128 int8 elements), staged
 // in LDS by the gfx950 global_load_lds DMA into a 2-stage ring with an
 // XOR-swizzled 16-byte chunk layout, v_mfma_f32_16x16x32_bf16 or
@@ -590,15 +590,16 @@ hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const int32
   if (a_scales)
     return launch_gg<true, 4, 4, false, 256, 2>(a, a_scales, ident_a, ident_m, w0, w1, offs, G, M,
                                                 N, K, swiglu, out, tile_start, s);
-  // bf16 A with at most 320 rows per group on average (e.g. T = 1571-2048
-  // routed top-8 over 64 experts, or 8 groups of T rows): 128 x 512 tiles.
-  // Against 256 x 256 they pad a group's last row tile less and leave less of
-  // a tail round; against 128 x 256 they move 40 instead of 48 bytes per
-  // K step per 1024 MFMA cycles.  The pipelined loop with 8 waves of 64 x
-  // 128, as below.  Measured at T = 1571 / 2048: int8 run() 2.82 / 3.27 ms
-  // against 2.93 / 3.44 with plain-loop 128 x 256 tiles; at T = 8192 they
-  // are 5-10% slower than 256 x 256.
-  if ((long long)M <= 320ll * G)
+  // bf16 A with at most 128 rows per group on average (e.g. T = 512 routed
+  // top-8 over 64 experts): 128 x 512 tiles, which pad a small group's last
+  // row tile less than 256 x 256; against 128 x 256 they move 40 instead of 48
+  // bytes per K step per 1024 MFMA cycles.  The pipelined loop with 8 waves of
+  // 64 x 128, as below.  run() measured (ms, 128 x 512 / 256 x 256): spread
+  // routing T = 512 (64 rows per expert) int8 4.93 / 5.04, bf16 2.50 / 2.67;
+  // T = 1571 (196 rows) int8 5.69 / 5.46, bf16 3.80 / 3.29; the harness's
+  // routing (8 groups of T rows) T = 1571 int8 2.33 / 2.15, T = 2048 bf16
+  // 3.68 / 3.20.
+  if ((long long)M <= 128ll * G)
     return launch_gg<false, 2, 4, true, 128, 2, false, 512>(a, nullptr, ident_a, ident_m, w0, w1,
                                                             offs, G, M, N, K, swiglu, out,
                                                             tile_start, s, ex);
@@ -616,7 +617,7 @@ hipError_t launch_grouped_gemm_i8(const void* a, const float* a_rs, const int32_
                                   const float* w1s, const int32_t* offs, int G, int M, int N, int K,
                                   bool swiglu, void* out, int32_t* tile_start, hipStream_t s) {
   const GgExtra sc{a_rs, a_rs_idx, ident_rs, w0s, swiglu ? w1s : w0s};
-  if ((long long)M <= 320ll * G)
+  if ((long long)M <= 128ll * G)
     return launch_gg<false, 2, 4, true, 128, 2, true, 512>(a, nullptr, ident_a, ident_m, w0, w1,
                                                            offs, G, M, N, K, swiglu, out,
                                                            tile_start, s, sc);
