@@ -11,9 +11,11 @@
 //
 // Plan (the reference's plan_kernel builds per-group pointers for CUTLASS on
 // the device; here it is one scan): tile_start[g] = sum over g' < g of
-// ceil(m_g' / BM), on the device, so nothing waits for the host.  The grid
-// is sized by the bound sum ceil(m_g / BM) <= ceil(M / BM) + G; blocks past
-// the last tile return at once.
+// ceil(m_g' / BM), on the device, so nothing waits for the host.  Up to 256
+// groups every block scans the group ends itself (no plan launch); beyond,
+// gg_plan_kernel writes tile_start into the workspace first.  The grid is
+// sized by the bound sum ceil(m_g / BM) <= ceil(M / BM) + G; blocks past the
+// last tile return at once.
 //
 // Tiles: 256 rows x 256 weight rows (128 x 512 for groups of at most 128
 // rows on average), 128-byte K steps (64 bf16 or 128 int8 elements), staged
@@ -83,6 +85,33 @@ __global__ __launch_bounds__(1024) void gg_plan_kernel(const int* __restrict__ o
     __syncthreads();
   }
   if (G == 0 && threadIdx.x == 0) tile_start[0] = 0;
+}
+
+// Up to kScanG groups a block finds its group itself: one wave-wide scan of
+// the row-tile counts per 64 groups (a load or two from L2, shuffles and a
+// ballot), instead of a separate plan launch and a binary search over its
+// output (a chain of dependent loads at the start of every tile).
+constexpr int kScanG = 256;
+
+// Row tiles of group gi (ends clamped into [0, M], as the tile itself does);
+// 0 past G.
+__device__ __forceinline__ int group_tiles(const int* __restrict__ offs, int gi, int G, int M,
+                                           int bm) {
+  if (gi >= G) return 0;
+  const int lo = gi > 0 ? min(max(offs[gi - 1], 0), M) : 0;
+  const int hi = min(max(offs[gi], 0), M);
+  return hi > lo ? (hi - lo + bm - 1) / bm : 0;
+}
+
+// Inclusive wave scan.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int n = __shfl_up(v, o, 64);
+    if (lane >= o) v += n;
+  }
+  return v;
 }
 
 // silu(g) * u in fp32
@@ -185,28 +214,75 @@ __global__ __launch_bounds__(64 * WM * WN) void grouped_gemm_kernel(
   // leaves the bound's surplus on the last XCD and up to a round more on the
   // others: the T = 2048 shared down projection, 256 tiles, took 305 us.)
   // Logical tiles are numbered group by group: group g owns
-  // [tile_start[g] * n_tiles, tile_start[g+1] * n_tiles).
+  // [gstart * n_tiles, (gstart + mtg) * n_tiles), gstart = tile_start[g].
   const unsigned b = blockIdx.x;
-  const unsigned nreal = (unsigned)tile_start[G] * (unsigned)n_tiles;
+  const int lane0 = threadIdx.x & 63;
+  // total row tiles: from the plan (G > kScanG) or a scan of the group ends
+  int total_rt = 0, incl0 = 0, tiles0 = 0;  // incl0 / tiles0: groups 0..63, lane = group
+  if (G <= kScanG) {
+    for (int base = 0; base < G; base += 64) {
+      const int t = group_tiles(offs, base + lane0, G, M, BM);
+      const int incl = wave_incl_scan(t);
+      if (base == 0) {
+        incl0 = incl;
+        tiles0 = t;
+      }
+      total_rt += __shfl(incl, 63, 64);
+    }
+  } else {
+    total_rt = tile_start[G];
+  }
+  total_rt = __builtin_amdgcn_readfirstlane(total_rt);  // wave-uniform: keep it in an SGPR
+  const unsigned nreal = (unsigned)total_rt * (unsigned)n_tiles;
   const unsigned r = (nreal + 7u) >> 3;
   if ((b >> 3) >= r) return;
   const unsigned l = (b & 7u) * r + (b >> 3);
   if (l >= nreal) return;
   const int lt = (int)(l / (unsigned)n_tiles);
-  // group of this tile: the last g with tile_start[g] <= lt
-  int lo = 0, hi = G - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (tile_start[mid] <= lt) lo = mid; else hi = mid - 1;
+  // group g of row tile lt: gstart <= lt < gstart + mtg (the first group whose
+  // inclusive tile count exceeds lt; groups without tiles never qualify)
+  int g = 0, gstart = 0, mtg = 0;
+  if (G <= 64) {
+    const unsigned long long m = __ballot(lane0 < G && incl0 > lt);
+    g = __ffsll((long long)m) - 1;
+    mtg = __shfl(tiles0, g, 64);
+    gstart = __shfl(incl0, g, 64) - mtg;
+  } else if (G <= kScanG) {
+    int carry = 0;
+    for (int base = 0; base < G; base += 64) {
+      const int t = group_tiles(offs, base + lane0, G, M, BM);
+      const int incl = wave_incl_scan(t) + carry;
+      const unsigned long long m = __ballot(base + lane0 < G && incl > lt);
+      if (m) {
+        const int L = __ffsll((long long)m) - 1;
+        g = base + L;
+        mtg = __shfl(t, L, 64);
+        gstart = __shfl(incl, L, 64) - mtg;
+        break;
+      }
+      carry = __shfl(incl, 63, 64);
+    }
+  } else {
+    // the last g with tile_start[g] <= lt
+    int lo = 0, hi = G - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (tile_start[mid] <= lt) lo = mid; else hi = mid - 1;
+    }
+    g = lo;
+    gstart = tile_start[g];
+    mtg = tile_start[g + 1] - gstart;
   }
-  const int g = lo;
+  // wave-uniform results of shuffles: SGPRs, not VGPRs the K loop needs
+  g = __builtin_amdgcn_readfirstlane(g);
+  gstart = __builtin_amdgcn_readfirstlane(gstart);
+  mtg = __builtin_amdgcn_readfirstlane(mtg);
   // Inside a group, column blocks of kSuperN n-tiles, row tiles across each
   // block, n fastest: 32 consecutive tiles (one XCD's co-running blocks) are
   // 4 row tiles x 8 weight tiles, so each A slice and each weight slice of a
   // K step is fetched from HBM once and then reused from that XCD's L2.
   constexpr int kSuperN = 8;
-  const int mtg = tile_start[g + 1] - tile_start[g];
-  const int li = (int)l - tile_start[g] * n_tiles;
+  const int li = (int)l - gstart * n_tiles;
   const int nblk = li / (mtg * kSuperN);
   const int rem = li - nblk * mtg * kSuperN;
   const int ncols = min(kSuperN, n_tiles - nblk * kSuperN);
@@ -556,9 +632,11 @@ static hipError_t launch_gg(const void* a, const float* a_scales, const void* id
                             int K, bool swiglu, void* out, int32_t* tile_start, hipStream_t s,
                             GgExtra i8s = GgExtra{}) {
   constexpr int BK = I8 ? 128 : 64;  // K-step elements
-  hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, BM, tile_start);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (G > kScanG) {  // the kernel scans up to kScanG group ends itself
+    hipLaunchKernelGGL(gg_plan_kernel, dim3(1), dim3(1024), 0, s, offs, G, M, BM, tile_start);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   if (M == 0 || N == 0 || G == 0) return hipSuccess;
   const int n_tiles = n_tiles_of<BNT>(N, swiglu);
   const long long m_bound = ((long long)M + BM - 1) / BM + G;

@@ -71,6 +71,24 @@ def test_grouped_gemm_ragged(cuda, sizes, N, K):
     check_plain(got, a, w, np.cumsum(sizes))
 
 
+@pytest.mark.parametrize("G", [64, 65, 200, 256, 257, 300])
+def test_grouped_gemm_group_lookup_paths(cuda, G):
+    """Each block finds its group by a wave scan of the group ends (up to 64
+    groups in one pass, up to 256 in passes of 64) or, beyond 256 groups, from
+    the plan kernel's tile starts: all three agree with the oracle on ragged
+    groups with empty ones among them."""
+    rng = np.random.default_rng(G)
+    sizes = rng.integers(0, 40, size=G)
+    sizes[rng.random(G) < 0.3] = 0
+    sizes[-1] = 300  # a multi-tile last group
+    N, K = 128, 64
+    a, w = make(list(sizes), N, K, seed=G)
+    print("group lookup G=%d M=%d" % (G, int(sizes.sum())), flush=True)
+    got = M.grouped_gemm(a.to(cuda), w.to(cuda), inclusive(sizes, cuda))
+    torch.cuda.synchronize()
+    check_plain(got, a, w, np.cumsum(sizes))
+
+
 @pytest.mark.parametrize("sizes,N,K", [
     ([700, 0, 900], 256, 64),      # large groups (pipelined K loop), a single K step
     ([700, 0, 900], 200, 192),     # three K steps (odd), partial column tile
