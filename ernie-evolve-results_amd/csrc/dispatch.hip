@@ -7,7 +7,9 @@
 // are ranked by their flat index t*k + j, giving exactly
 // argsort(topk_ids.flatten(), stable) -- by expert, then ascending token.
 //
-// Three launches, all integer work over the T*k ids (1 MB at T=32768, k=8):
+// Three launches (two when E * blocks <= kSumMax: the index kernel then sums
+// the block histograms itself), all integer work over the T*k ids (1 MB at
+// T=32768, k=8):
 //   1. pair_hist:   per block of 256 pairs, one 64-bit LDS bitmask word per
 //                   (expert, wave) marks which pairs chose the expert; the
 //                   popcounts are the block's expert histogram.
@@ -125,16 +127,62 @@ __device__ __forceinline__ void lds_offsets(const int* __restrict__ cnt, int E, 
   if (tid == 0) offs[E] = total;
 }
 
+// Small problems (E * nblk <= kSumMax): dispatch_index_kernel reads the raw
+// block histograms itself -- each block sums, per expert, the counts of the
+// blocks before it and of all blocks -- so block_scan_kernel is not launched.
+// P = 256 / E lanes (a power of two, at most 64) share one expert's column.
+constexpr int kSumMax = 8192;
+
+__device__ __forceinline__ void column_sums(const int* __restrict__ blockcnt, int nblk, int E,
+                                            int* base_out, int* tot_out) {
+  const int tid = threadIdx.x;
+  int P = 64;
+  while (P > 1 && P * E > kPairsPerBlock) P >>= 1;
+  const int per = kPairsPerBlock / P;  // experts handled per pass
+  for (int e0 = 0; e0 < E; e0 += per) {
+    const int e = e0 + tid / P, j = tid % P;
+    int before = 0, all = 0;
+    if (tid / P < per && e < E) {
+      const int* col = blockcnt + (long long)e * nblk;
+      for (int i = j; i < nblk; i += P) {
+        const int c = col[i];
+        all += c;
+        if (i < (int)blockIdx.x) before += c;
+      }
+    }
+    // reduce over the P lanes of the expert (P divides 64: groups never straddle a wave)
+    for (int o = P >> 1; o > 0; o >>= 1) {
+      before += __shfl_xor(before, o, 64);
+      all += __shfl_xor(all, o, 64);
+    }
+    if (tid / P < per && e < E && j == 0) {
+      base_out[e] = before;
+      tot_out[e] = all;
+    }
+  }
+}
+
+// SUM = false: blockbase is block_scan_kernel's scanned columns and totals its
+// per-expert totals.  SUM = true: blockbase is pair_hist_kernel's raw block
+// histograms, summed here (totals unused).
+template <bool SUM>
 __global__ __launch_bounds__(kPairsPerBlock) void dispatch_index_kernel(
     const int* __restrict__ ids, long long npairs, int E, int k, int nblk,
     const int* __restrict__ blockbase, const int* __restrict__ totals,
     int* __restrict__ row_token, int* __restrict__ pair_row, int* __restrict__ offsets_out,
     int* __restrict__ counts_out) {
   extern __shared__ unsigned long long mask[];
-  int* offs = reinterpret_cast<int*>(mask + E * kMaskWords);
+  int* offs = reinterpret_cast<int*>(mask + E * kMaskWords);  // [E + 1]
+  int* sbase = offs + E + 1;                                   // SUM: [E] rows of e before this block
+  int* stot = sbase + E;                                       // SUM: [E] totals
   __shared__ int sh4[4];
   const int tid = threadIdx.x;
   for (int i = tid; i < E * kMaskWords; i += kPairsPerBlock) mask[i] = 0ull;
+  if (SUM) {
+    column_sums(blockbase, nblk, E, sbase, stot);
+    __syncthreads();
+    totals = stot;
+  }
   lds_offsets(totals, E, offs, sh4);  // contains __syncthreads
   int e;
   build_masks(ids, npairs, E, mask, e);
@@ -155,7 +203,7 @@ __global__ __launch_bounds__(kPairsPerBlock) void dispatch_index_kernel(
   const unsigned long long* me = mask + e * kMaskWords;
   int rank = __popcll(me[wv] & ((1ull << bit) - 1ull));
   for (int w = 0; w < wv; ++w) rank += __popcll(me[w]);
-  const int pos = offs[e] + blockbase[(long long)e * nblk + blockIdx.x] + rank;
+  const int pos = offs[e] + (SUM ? sbase[e] : blockbase[(long long)e * nblk + blockIdx.x]) + rank;
   pair_row[p] = pos;
   row_token[pos] = (int)(p / k);
 }
@@ -198,12 +246,21 @@ hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_
                      npairs, E, nblk, blockcnt);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
+  if ((long long)E * nblk <= kSumMax) {
+    // few block histograms: every index block sums them itself, no scan launch
+    const size_t shm_sum = shm_hist + sizeof(int) * (3 * E + 1);
+    hipLaunchKernelGGL(dispatch_index_kernel<true>, dim3(nblk), dim3(kPairsPerBlock), shm_sum, s,
+                       ids, npairs, E, k, nblk, blockcnt, totals, row_token, pair_row, offsets,
+                       counts);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(block_scan_kernel, dim3(E), dim3(256), 0, s, blockcnt, nblk, totals);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
   const size_t shm_idx = shm_hist + sizeof(int) * (E + 1);
-  hipLaunchKernelGGL(dispatch_index_kernel, dim3(nblk), dim3(kPairsPerBlock), shm_idx, s, ids,
-                     npairs, E, k, nblk, blockcnt, totals, row_token, pair_row, offsets, counts);
+  hipLaunchKernelGGL(dispatch_index_kernel<false>, dim3(nblk), dim3(kPairsPerBlock), shm_idx, s,
+                     ids, npairs, E, k, nblk, blockcnt, totals, row_token, pair_row, offsets,
+                     counts);
   return hipGetLastError();
 }
 
