@@ -7,7 +7,7 @@
 //   * gathered rows equal x[row_token];
 //   * with identity experts (y = xg) the combine returns x * sum_j w_j.
 // This is what a C++ caller of the reference's run() (kernel.cu:4067-4077)
-// would write; INTEGRATION.md shows the same calls inside run().
+// would write; moe_route.run() makes the same calls from Python.
 //
 // Build (done by moe_route.build): g++ -O2 -std=c++17 moe_step.cpp
 //   -I include -I /opt/rocm/include -D__HIP_PLATFORM_AMD__ -L <lib dir> -lmoe_route

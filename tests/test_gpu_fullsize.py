@@ -1,4 +1,4 @@
-"""Full-size (BASELINE.json shapes) GPU checks through size-independent
+"""Full-size (the C2-C5 benchmark shapes) GPU checks through size-independent
 properties: selection exactness on the GPU's own logits, histogram/offset
 consistency, permutation bijection + stability, bit-equal gathered rows,
 fp8 rows against the oracle on a sample, combine against a torch fp32
