@@ -137,7 +137,8 @@ int moe_combine(const void* y, int y_dtype, const int32_t* pair_row, const float
                 const void* shared, int T, int H, int k, void* out, void* stream);
 
 /* Workspace bytes moe_grouped_gemm / moe_grouped_swiglu need: the device
- * tile plan, (G+1) int32. */
+ * tile plan, (G+1) int32.  It is always required; the kernels only write and
+ * read it for G > 256 (below, every block scans the group ends itself). */
 size_t moe_grouped_gemm_workspace_bytes(int G);
 
 /* Expert grouped GEMM over expert-contiguous rows.  Replaces grouped_mm
