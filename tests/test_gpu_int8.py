@@ -29,6 +29,8 @@ def inclusive(sizes, dev):
     (5, 16, 0, 1.0), (33, 3584, 0, 1.0), (33, 3584, 128, 1.0), (17, 8192, 0, 1.0),
     (17, 8192, 128, 1.0 / 128), (3, 16384, 128, 0.5), (9, 4224, 128, 1.0),
     (33, 3584, 16, 1.0 / 16), (6, 8192, 16, 1.0), (5, 48, 16, 1.0), (7, 12304, 16, 1.0),
+    # widths whose K / 16 leaves part of the 256-thread block idle
+    (9, 512, 16, 1.0), (5, 1536, 0, 0.5), (70, 3584, 0, 1.0), (3, 7680, 16, 1.0 / 16),
 ])
 def test_quant_rows_bit_exact(cuda, R, K, had, mul):
     g = torch.Generator().manual_seed(R * 7 + K)
@@ -43,15 +45,16 @@ def test_quant_rows_bit_exact(cuda, R, K, had, mul):
     assert np.array_equal(s.cpu().numpy(), rs)
 
 
-def test_quant_rows_group_gating(cuda):
-    G, rows, K = 4, 6, 256
+@pytest.mark.parametrize("K,had", [(256, 128), (3584, 16)])
+def test_quant_rows_group_gating(cuda, K, had):
+    G, rows = 4, 6
     x = torch.randn(G * rows, K).to(torch.bfloat16)
     counts = torch.tensor([3, 0, 1, 0], dtype=torch.int32, device=cuda)
     q = torch.full((G * rows, K), 99, dtype=torch.int8, device=cuda)
     s = torch.full((G * rows,), -1.0, device=cuda)
-    M.quant_rows_i8(x.to(cuda), hadamard=128, group_rows=rows, group_counts=counts, q=q, scales=s)
+    M.quant_rows_i8(x.to(cuda), hadamard=had, group_rows=rows, group_counts=counts, q=q, scales=s)
     torch.cuda.synchronize()
-    rq, rs = O.quant_rows_i8(x, hadamard=128)
+    rq, rs = O.quant_rows_i8(x, hadamard=had)
     for gi, c in enumerate([3, 0, 1, 0]):
         sl = slice(gi * rows, (gi + 1) * rows)
         if c:
