@@ -61,7 +61,7 @@ hipError_t launch_combine(const void* y, int y_dtype, const int32_t* pair_row, c
 // Column tiles of the grouped GEMM for N output columns.
 int grouped_gemm_n_tiles(int N, bool swiglu);
 // Expert grouped GEMM (plain or SwiGLU epilogue); tile_start is [G+1] ints of
-// workspace; a_scales != NULL selects an e4m3fn A with [M, K/128] fp32 scales;
+// workspace (used only for G > 256); a_scales != NULL selects an e4m3fn A with [M, K/128] fp32 scales;
 // a_rows (bf16 A, may be NULL) maps operand row r to row a_rows[r] of a.
 hipError_t launch_grouped_gemm(const void* a, const float* a_scales, const int32_t* a_rows,
                                const void* ident_a, int ident_m, const void* w0, const void* w1,
