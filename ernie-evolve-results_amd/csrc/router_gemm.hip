@@ -9,14 +9,17 @@
 // Tiles are brought into LDS by the gfx950
 // global_load_lds_dwordx4 DMA (no register staging), into an NS-stage ring
 // with an XOR-swizzled 16-byte-chunk layout (conflict-free fragment reads),
-// one s_barrier per K step.  At N = 256 a 512-thread block owns 256 rows x
-// all 256 experts: the router weight (3.7 MB) is then re-read from L2 once
-// per 256 rows instead of once per 128, which halved the kernel's time on
-// MI355X.  To still fill 256 CUs at T = 32768 the K range is split in two
-// (split-K); the two fp32 partial sums land side by side as [T, 2N] and the
-// scoring kernel adds them in a fixed order (deterministic, no atomics).
-// 16 waves (4 per SIMD, 64x64 accumulator tiles) hide the DMA latency better
-// than 8 waves with 128x64 tiles (measured 122 vs 141 us at T = 32768).
+// one s_barrier per K step.  At N >= 256 a 1024-thread block (16 waves of
+// 64 x 32 accumulators) owns 256 rows x 128 experts with a 3-stage ring (two
+// stages in flight, 144 KB of LDS): at T = 32768, E = 256 the 128 row tiles x
+// 2 expert tiles fill 256 CUs without splitting K, and the two blocks of a
+// row tile (neighbouring hardware ids, the same XCD) read their x rows once
+// from HBM and once from L2.  The earlier 256 x 256 tile with a 2-stage ring
+// needed split-K = 2 to fill the chip and waited on each K step's DMA (route
+// stage 202 against 189 us in the C4 step).  When the row tiles alone leave
+// the chip idle (small T), the K range is still split: the fp32 partial sums
+// land side by side as [T, ksplit * N] and the scoring kernel adds them in a
+// fixed order (deterministic, no atomics).
 // x is loaded with ordinary (temporal) loads although the GEMM reads it once:
 // the part of x still held in the 256 MB memory-side cache (MALL) when the
 // permute reads x again is not fetched from HBM a second time.  Measured on
@@ -178,14 +181,14 @@ static hipError_t launch_dma(const __bf16* x, const __bf16* w, int T, int H, int
 }
 
 // Tile configuration per N, and the K partition count that fills the chip.
-//   N >= 256: 256 x 256 tile, 16 waves (W re-read once per 256 rows)
+//   N >= 256: 256 x 128 tile, 16 waves, 3 stages (W re-read once per 256 rows)
 //   N = 128, 64, 32: 64-row tiles, 4 waves (W is small and stays in L2)
 //   N = 16 / 8: 32 x 16 tile, 2 waves (a pure x stream)
 // ksplit doubles while blocks * ksplit is below the target and H still
 // splits into whole 64-wide K steps; the partial sums are [T, ksplit*N].
 struct GemmTile { int bm, bn, target; };
 static GemmTile gemm_tile(int N) {
-  if (N >= 256) return {256, 256, 256};
+  if (N >= 256) return {256, 128, 256};
   if (N >= 32) return {64, N, 256};
   return {32, 16, 1024};
 }
@@ -202,7 +205,7 @@ int router_gemm_ksplit(int T, int H, int N) {
 // the caller); H % (64 * ksplit) == 0.
 hipError_t launch_router_gemm(const __bf16* x, const __bf16* w, int T, int H, int N, int ksplit,
                               float* out, hipStream_t s) {
-  if (N >= 256) return launch_dma<256, 256, 2, 4, 4>(x, w, T, H, N, ksplit, out, s);
+  if (N >= 256) return launch_dma<256, 128, 3, 4, 4>(x, w, T, H, N, ksplit, out, s);
   if (N == 128) return launch_dma<64, 128, 3, 1, 4>(x, w, T, H, N, ksplit, out, s);
   if (N == 64) return launch_dma<64, 64, 3, 2, 2>(x, w, T, H, N, ksplit, out, s);
   if (N == 32) return launch_dma<64, 32, 3, 4, 1>(x, w, T, H, N, ksplit, out, s);
