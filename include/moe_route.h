@@ -72,8 +72,14 @@ int moe_version(void);
  * Replaces TORCH_CHECK's exception text (K:1771-1775, K:4088). */
 const char* moe_last_error_string(void);
 
-/* Workspace bytes moe_route needs.  w_dtype FP32 adds the hi/lo split weight
- * [2E,H] bf16 and the packed logits [T,2E] fp32 (K:4197-4268 arena). */
+/* Workspace bytes moe_route needs (the K:4197-4268 arena, caller-owned).
+ * Non-zero only when
+ *   - w_dtype is FP32: the hi/lo split weight [2E,H] bf16, plus
+ *   - the GEMM writes more than one partial logit block per row, i.e. FP32
+ *     weights (hi and lo halves) or a K split (ksplit > 1, chosen when the
+ *     row x expert tiles alone leave the chip's 256 CUs idle, e.g. small T):
+ *     [T, parts*E] fp32 partial sums.
+ * The DeepSeek-V3 shape with bf16 weights (T=32768, H=7168, E=256) needs 0. */
 size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype);
 
 /* Stage 1: router GEMM, logits[T,E] fp32 = x[T,H] bf16 . w[E,H]^T bf16, fp32

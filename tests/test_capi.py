@@ -104,6 +104,26 @@ def test_permute_and_combine_validation():
     err(L.moe_router_gemm(FAKE, FAKE, 4, 96, 8, FAKE, None), -3)
 
 
+def _router_ksplit(T, H, N):
+    """K partitions of the router GEMM: the tile rule of router_gemm.hip
+    (row x expert tiles 256x128 for N >= 256, 64xN for 32 <= N <= 128, 32x16
+    below; K halves while blocks * ksplit stay under the fill target)."""
+    bm, bn, target = (256, 128, 256) if N >= 256 else (64, N, 256) if N >= 32 else (32, 16, 1024)
+    blocks = -(-T // bm) * -(-N // bn)
+    ks = 1
+    while blocks * ks < target and ks < 8 and H % (64 * ks * 2) == 0:
+        ks *= 2
+    return ks
+
+
+def _route_ws(T, H, E, fp32):
+    r256 = lambda b: (b + 255) // 256 * 256
+    N = 2 * E if fp32 else E
+    parts = (N // E) * _router_ksplit(T, H, N)
+    b = r256(2 * E * H * 2) if fp32 else 0
+    return b + (r256(T * parts * E * 4) if parts > 1 else 0)
+
+
 def test_workspace_sizes():
     L = M.lib()
     # small N: 32-row tiles, 4 blocks at T=100 -> K split in 2 (H=128 allows no more)
@@ -112,9 +132,15 @@ def test_workspace_sizes():
     # fp32 weights: [2E,H] bf16 split (4096 B) + [T, 2 halves * 2 K parts * E] fp32
     assert L.moe_route_workspace_bytes(100, 128, 8, 1) == 4096 + 12800
     assert L.moe_route_workspace_bytes(100, 64, 8, 0) == 0        # H=64: one K step, no split
-    # DeepSeek-V3 shape: the GEMM splits K in two -> [T, 2E] fp32 partial sums
-    assert L.moe_route_workspace_bytes(32768, 7168, 256, 0) == 32768 * 2 * 256 * 4
+    # DeepSeek-V3 shape: 128 row tiles x 2 expert tiles fill the chip, no split, no workspace
+    assert L.moe_route_workspace_bytes(32768, 7168, 256, 0) == 0
+    # ... but fp32 weights there still need the [2E,H] split and [T, 2E] hi/lo partial logits
+    assert L.moe_route_workspace_bytes(32768, 7168, 256, 1) == 2 * 256 * 7168 * 2 + 32768 * 512 * 4
     assert L.moe_route_workspace_bytes(65536, 7168, 256, 0) == 0
+    for T, H, E in [(1, 64, 8), (100, 128, 8), (512, 1024, 8), (8192, 4096, 8), (16384, 2048, 128),
+                    (1571, 8192, 64), (32768, 7168, 256), (300, 7168, 256), (4096, 8192, 64)]:
+        for fp32 in (0, 1):
+            assert L.moe_route_workspace_bytes(T, H, E, fp32) == _route_ws(T, H, E, fp32), (T, H, E, fp32)
     # T*k = 32768*8 pairs -> 1024 blocks of 256; [E, nblk] + [E] int32
     assert L.moe_permute_workspace_bytes(32768, 256, 8) == 256 * 1024 * 4 + 1024
 
