@@ -12,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "../../include/moe_route.h"
 #include "moe_common.h"
@@ -198,9 +199,12 @@ size_t moe_permute_workspace_bytes(int T, int E, int k) {
   return round256((size_t)E * nblk * 4) + round256((size_t)E * 4);
 }
 
-int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H, int E, int k,
-                int out_dtype, void* xg, float* scales, int32_t* row_token, int32_t* pair_row,
-                int32_t* offsets, int32_t* counts, void* ws, size_t ws_bytes, void* stream) {
+}  // extern "C"
+
+// Argument checks of moe_permute, everything except the workspace.
+static int check_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H, int E,
+                         int k, int out_dtype, void* xg, float* scales, int32_t* row_token,
+                         int32_t* pair_row) {
   if (T < 0 || H <= 0) return fail(MOE_ERR_INVALID_ARG, "T=%d, H=%d", T, H);
   if (E < 1 || E > 1024) return fail(MOE_ERR_INVALID_ARG, "E=%d not in [1, 1024]", E);
   if (k < 1 || k > 8) return fail(MOE_ERR_INVALID_ARG, "k=%d not in [1, 8]", k);
@@ -229,11 +233,19 @@ int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int 
       return fail(MOE_ERR_UNSUPPORTED, "T*H too large for one call (%lld vectors)",
                   (long long)T * H * elem / 16);
   }
-  const size_t need = moe_permute_workspace_bytes(T, E, k);
-  if (!ws || ws_bytes < need)
-    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
   if (((long long)T * k) >= (1ll << 31))
     return fail(MOE_ERR_UNSUPPORTED, "T*k=%lld exceeds int32 rows", (long long)T * k);
+  return MOE_OK;
+}
+
+// The permute's launches over a validated workspace of
+// moe_permute_workspace_bytes(T, E, k) bytes.
+static int permute_launch(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H,
+                          int E, int k, int out_dtype, void* xg, float* scales,
+                          int32_t* row_token, int32_t* pair_row, int32_t* offsets,
+                          int32_t* counts, void* ws, void* stream) {
+  const bool fp8 = out_dtype == MOE_DTYPE_FP8E4M3FN;
+  const int elem = x_dtype == MOE_DTYPE_BF16 ? 2 : 4;
   hipStream_t s = (hipStream_t)stream;
   const int nblk = moe::dispatch_blocks((long long)T * k);
   int32_t* blockcnt = (int32_t*)ws;
@@ -244,6 +256,83 @@ int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int 
   if (rc || !xg || T == 0) return rc;
   if (fp8) return launched(moe::launch_gather_fp8(x, pair_row, T, H, k, xg, scales, s), "gather_fp8");
   return launched(moe::launch_gather(x, elem, pair_row, T, H, k, xg, s), "gather");
+}
+
+// ---------------------------------------------------------------------------
+// Fixed device scratch of moe_permute_noalloc: the per-block expert
+// histograms and expert totals that moe_permute keeps in the caller's
+// workspace.  One copy per GPU, held until the process ends.  Host code never
+// names the array in a launch or copy: it uses the address
+// hipGetSymbolAddress reports for the current device, looked up once per
+// device on the first call there.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoallocScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];
+
+static int noalloc_scratch(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return launched(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(MOE_ERR_UNSUPPORTED, "device %d beyond the %d scratch slots", dev,
+                kMaxScratchDevices);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess) return launched(e, "hipStreamGetDevice");
+    if ((int)sdev != dev)
+      return fail(MOE_ERR_INVALID_ARG, "stream belongs to device %d, current device is %d",
+                  (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return launched(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                                               "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOE_OK;
+}
+
+extern "C" {
+
+int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H, int E, int k,
+                int out_dtype, void* xg, float* scales, int32_t* row_token, int32_t* pair_row,
+                int32_t* offsets, int32_t* counts, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_permute(x, x_dtype, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
+                         pair_row);
+  if (rc) return rc;
+  const size_t need = moe_permute_workspace_bytes(T, E, k);
+  if (!ws || ws_bytes < need)
+    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
+  return permute_launch(x, x_dtype, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
+                        pair_row, offsets, counts, ws, stream);
+}
+
+size_t moe_permute_noalloc_max_scratch_bytes(void) { return kNoallocScratchBytes; }
+
+int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H, int E,
+                        int k, int out_dtype, void* xg, float* scales, int32_t* row_token,
+                        int32_t* pair_row, int32_t* offsets, int32_t* counts, void* stream) {
+  int rc = check_permute(x, x_dtype, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
+                         pair_row);
+  if (rc) return rc;
+  const size_t need = moe_permute_workspace_bytes(T, E, k);
+  if (need > kNoallocScratchBytes)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "T=%d, E=%d, k=%d needs %zu bytes of scratch, above the fixed %zu "
+                "(use moe_permute with a workspace)",
+                T, E, k, need, kNoallocScratchBytes);
+  void* ws = nullptr;
+  if ((rc = noalloc_scratch(stream, &ws))) return rc;
+  return permute_launch(x, x_dtype, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
+                        pair_row, offsets, counts, ws, stream);
 }
 
 int moe_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* topk_w,

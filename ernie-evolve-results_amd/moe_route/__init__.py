@@ -34,7 +34,8 @@ EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
            "moe_grouped_gemm_workspace_bytes", "moe_grouped_gemm", "moe_grouped_swiglu",
            "moe_grouped_gemm_fp8", "moe_grouped_swiglu_fp8", "moe_quant_rows_i8",
            "moe_grouped_gemm_i8", "moe_grouped_swiglu_i8", "moe_grouped_gemm_rows",
-           "moe_grouped_swiglu_rows"]
+           "moe_grouped_swiglu_rows", "moe_permute_noalloc_max_scratch_bytes",
+           "moe_permute_noalloc"]
 
 
 class MoeError(RuntimeError):
@@ -84,6 +85,11 @@ def lib():
         L.moe_permute.restype = _I
         L.moe_permute.argtypes = [_P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _Z,
                                   _P]
+        L.moe_permute_noalloc_max_scratch_bytes.restype = _Z
+        L.moe_permute_noalloc_max_scratch_bytes.argtypes = []
+        L.moe_permute_noalloc.restype = _I
+        L.moe_permute_noalloc.argtypes = [_P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P,
+                                          _P]
         L.moe_combine.restype = _I
         L.moe_combine.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]
         L.moe_grouped_gemm_workspace_bytes.restype = _Z

@@ -134,6 +134,23 @@ int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int 
                 int32_t* pair_row, int32_t* offsets, int32_t* counts, void* ws,
                 size_t ws_bytes, void* stream);
 
+/* moe_permute without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, hosts
+ * that forbid hipMalloc).  No counterpart in the reference (whose run()
+ * takes scratch from a per-call arena, K:4197-4268).  Same arguments,
+ * results and errors as moe_permute; the per-block histograms live in a
+ * fixed device array of moe_permute_noalloc_max_scratch_bytes() (4 MiB) per
+ * GPU, held until the process ends, so moe_permute_workspace_bytes(T, E, k)
+ * must not exceed it (E=256, k=8: T up to 131040) -- larger calls return
+ * MOE_ERR_UNSUPPORTED.  Nothing in it needs clearing between calls (every
+ * call writes all it reads).  The array is shared by every call on one GPU:
+ * calls that overlap on one GPU (two streams, two threads) race.  stream
+ * must belong to the calling thread's current device. */
+size_t moe_permute_noalloc_max_scratch_bytes(void);
+int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H, int E,
+                        int k, int out_dtype, void* xg, float* scales, int32_t* row_token,
+                        int32_t* pair_row, int32_t* offsets, int32_t* counts, void* stream);
+
 /* Stage 5: weighted combine.  Replaces combine_kernel K:2365-2428:
  *   out[t] = cast(shared[t] + sum_j topk_w[t,j] * y[pair_row[t,j]])
  * accumulated in fp32 in slot order.  y [R,H] and out [T,H] of y_dtype (BF16

@@ -312,3 +312,28 @@ def test_error_string_is_thread_local():
         t.join()
     assert got["a"][0] == -3 and "E=12" in got["a"][1]
     assert got["b"][0] == -3 and "E=24" in got["b"][1]
+
+
+def test_permute_noalloc_validation():
+    """The allocation-free permute shares moe_permute's checks and refuses
+    sizes whose histograms exceed its fixed device scratch -- before any HIP
+    call, so this runs without a GPU."""
+    L = M.lib()
+    cap = L.moe_permute_noalloc_max_scratch_bytes()
+    assert cap == 4 << 20
+    def perm(T=8, H=256, E=16, k=2, od=0, sc=None, x=FAKE, rt=FAKE):
+        return L.moe_permute_noalloc(x, 0, FAKE, T, H, E, k, od, FAKE, sc, rt, FAKE, None, None,
+                                     None)
+    err(perm(od=1), -3, "out_dtype")
+    err(perm(od=2), -1, "scales")
+    err(perm(H=4), -6)
+    err(perm(E=0), -2)
+    err(perm(k=9), -2)
+    err(perm(rt=None), -1)
+    err(perm(x=None), -1)
+    # largest T that fits at E=256, k=8: ceil(T*8/256) blocks x 256 experts x 4 B + 1 KiB
+    T_max = ((cap - 1024) // (256 * 4)) * 32
+    assert L.moe_permute_workspace_bytes(T_max, 256, 8) <= cap
+    assert L.moe_permute_workspace_bytes(T_max + 1, 256, 8) > cap
+    assert T_max == 131040
+    err(perm(T=T_max + 1, H=7168, E=256, k=8), -3, "scratch")
