@@ -1,0 +1,359 @@
+// Stages 1+2 in one kernel at E = 256: router GEMM + scoring + top-k +
+// histogram, with the logits tile kept on chip.
+//
+// Replaces the reference's cublasGemmEx (K:4327-4339) followed by
+// topk_kernel (K:1829-1920), which writes the [T,E] fp32 logits to HBM and
+// reads them back.  Here a workgroup owns 128 tokens x all 256 experts:
+//
+//   weights     a small pre-pass copies w[256, H] into a fragment-major
+//               layout, so every MFMA B fragment a wave loads is 1 KB
+//               contiguous (the row-major rows are 14 KB apart and land on
+//               few L2 channels: the weight stream ran at ~2/3 of the speed).
+//   main loop   x[128, 64-wide K step] is brought into an LDS ring by the
+//               gfx950 global_load_lds DMA, D = 4 steps ahead.  Each of the
+//               8 waves (two per SIMD: one wave alone cannot issue MFMAs at
+//               the matrix core's rate) owns 32 experts, so its weight slice
+//               is private and goes straight to registers, also D steps
+//               ahead.  v_mfma_f32_16x16x32_bf16, fp32 accumulate, K in the
+//               same order as the standalone GEMM (identical logits).  x and
+//               w loads share the in-order vmcnt counter: waiting for a
+//               step's weights retires its x stage too, and a wave never has
+//               more than 63 loads in flight (the counter's limit).
+//   epilogue    the 128 x 256 fp32 tile goes through LDS once; 16 lanes per
+//               token score it (the scoring kernel's per-token routine,
+//               bit-identical selection), write router_logits row by row,
+//               the ids and weights, and the block's expert histogram.
+#include "moe_common.h"
+#include "score_token.h"
+
+namespace moe {
+
+namespace rf {
+constexpr int BM = 128, E = 256, BK = 64, ROWB = BK * 2, CH = 8;
+constexpr int STAGE_B = BM * ROWB;        // 16 KB of x per K step
+constexpr int TILE_LD = E + 4;            // fp32 tile row stride (floats) in the epilogue
+constexpr int TILE_B = BM * TILE_LD * 4;  // 133 KB
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & (CH - 1); }
+}  // namespace rf
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
+// bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Eight 16-byte LDS reads 2 KB apart, issued as one instruction group the
+// compiler does not track; the caller places the lgkmcnt wait (an asm that
+// takes the eight registers as "+v" operands, so nothing reads them before it).
+__device__ __forceinline__ void lds_read8(bf16x8 (&d)[8], unsigned ad) {
+  asm volatile(
+      "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:2048\n\t"
+      "ds_read_b128 %2, %8 offset:4096\n\tds_read_b128 %3, %8 offset:6144\n\t"
+      "ds_read_b128 %4, %8 offset:8192\n\tds_read_b128 %5, %8 offset:10240\n\t"
+      "ds_read_b128 %6, %8 offset:12288\n\tds_read_b128 %7, %8 offset:14336"
+      : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]),
+        "=&v"(d[6]), "=&v"(d[7])
+      : "v"(ad)
+      : "memory");
+}
+
+// Bytes of LDS the kernel needs: the x ring or the epilogue tile.
+constexpr int route_fused_lds(int D) {
+  return (D + 1) * rf::STAGE_B > rf::TILE_B ? (D + 1) * rf::STAGE_B : rf::TILE_B;
+}
+
+// NWV waves (64 * NWV threads, NWV / 4 per SIMD).  KS = 1: wave w owns experts
+// [w*WE, (w+1)*WE) of all 128 rows, both 32-wide K halves of every step.
+// KS = 2: the two waves of a SIMD own the same 64 experts and split every step
+// into its two K halves (wave w does half w / 4); their partial tiles are
+// added in LDS at the end.  Either way a wave's weight slice is its own and
+// goes straight to registers, and x is shared through the LDS ring.
+template <int NWV, int KS, int D, int KTC, int V, int KK, int SC>
+__global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
+    const __bf16* __restrict__ x, const __bf16* __restrict__ wf, const float* __restrict__ bias,
+    int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
+    float norm_min, float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ wout,
+    int* __restrict__ counts) {
+  using namespace rf;
+  constexpr int NT = 64 * NWV;             // threads
+  constexpr int NG = NWV / KS;             // expert groups (waves per K half)
+  constexpr int WE = E / NG;               // experts per wave
+  constexpr int NJ = WE / 16;              // 16-expert fragment columns per wave
+  constexpr int KH = 2 / KS;               // 32-wide K halves per wave per step
+  constexpr int NX = (BM / 8) / NWV;       // x DMA instructions per wave per stage
+  constexpr int NWF = KH * NJ;             // weight fragments per wave per step
+  constexpr int NS = D + 1;                // x ring stages
+  static_assert(KS == 1 || NWV == 8, "the K split pairs the two waves of a SIMD");
+  // every wave keeps at most 63 vector loads in flight (the vmcnt limit: the
+  // counter does not account for more)
+  static_assert(D * (NX + NWF) <= 63, "too many loads in flight per wave");
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wg = wave % NG;                // expert group
+  const int kw = wave / NG;                // K half (KS = 2)
+  const long long m0 = (long long)blockIdx.x * BM;
+  const int KT = KTC > 0 ? KTC : H / BK;
+  const int fr = lane & 15, fc = lane >> 4;
+
+  // x DMA sources (rows past T clamped: loaded, never stored)
+  const __bf16* xsrc[NX];
+#pragma unroll
+  for (int q = 0; q < NX; ++q) {
+    const int gi = wave * NX + q;
+    const int r = gi * 8 + lane / 8, p = lane % 8;
+    long long row = m0 + r;
+    if (row >= T) row = T - 1;
+    xsrc[q] = x + row * H + (p ^ swz(r)) * 8;
+  }
+
+  // x step `src_kt` into the ring slot of step `kt`
+  auto issue_x = [&](int kt, int src_kt) {
+    char* st = lds + (kt % NS) * STAGE_B;
+#pragma unroll
+    for (int q = 0; q < NX; ++q) {
+      auto* dst = (__attribute__((address_space(3))) void*)(st + (wave * NX + q) * 1024);
+      __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + src_kt * BK), dst, 16, 0, 0);
+    }
+  };
+  bf16x8 wr[D][NWF];
+  auto issue_w = [&](int kt, bf16x8 (&dst)[NWF]) {
+#pragma unroll
+    for (int h = 0; h < KH; ++h) {
+      const int kk = KS == 2 ? kw : h;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        dst[h * NJ + j] = *reinterpret_cast<const bf16x8*>(
+            wf + ((long long)((kt * 2 + kk) * 16 + wg * NJ + j) * 64 + lane) * 8);
+    }
+  };
+  constexpr int VMW = (D - 1) * (NX + NWF);
+
+  f32x4 acc[8][NJ];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // prologue: steps 0 .. D-1 in flight (KT % D == 0 is required by the launcher)
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    issue_x(u, u);
+    issue_w(u, wr[u]);
+  }
+
+  // Every step waits, computes and refills the same way: the last D steps
+  // reload step KT-1 into slots nobody reads again, so the compiler sees one
+  // uniform sequence and the vmcnt count below holds on every step.
+#pragma unroll
+  for (int kb = 0; kb < KT; kb += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int kt = kb + u;
+      // stage kt and weights kt are the oldest loads once at most (D-1)
+      // later steps' loads are pending.  The wait is the builtin, not asm,
+      // so the compiler's own vmcnt bookkeeping knows they are retired.
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(VMW));
+      __builtin_amdgcn_s_barrier();
+      const char* sb = lds + (kt % NS) * STAGE_B;
+      // rows i*16 + fr share the swizzle of fr: a half step's eight fragment
+      // reads are 2 KB apart
+      auto frag_addr = [&](int kk) {
+        return (unsigned)(uintptr_t)((__attribute__((address_space(3))) const char*)(
+            sb + fr * ROWB + (((kk * 4 + fc) ^ swz(fr)) * 16)));
+      };
+      bf16x8 a0[8], a1[8];
+      lds_read8(a0, frag_addr(KS == 2 ? kw : 0));
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(a0[0]), "+v"(a0[1]), "+v"(a0[2]), "+v"(a0[3]), "+v"(a0[4]),
+                     "+v"(a0[5]), "+v"(a0[6]), "+v"(a0[7])::"memory");
+      // with both halves: the second half's reads go out before the first
+      // half's MFMAs and land while they run
+      if constexpr (KH == 2) lds_read8(a1, frag_addr(1));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], wr[u][j], acc[i][j], 0, 0, 0);
+      if constexpr (KH == 2) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(a1[0]), "+v"(a1[1]), "+v"(a1[2]), "+v"(a1[3]), "+v"(a1[4]),
+                       "+v"(a1[5]), "+v"(a1[6]), "+v"(a1[7])::"memory");
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[i][j] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], wr[u][NJ + j], acc[i][j], 0, 0, 0);
+      }
+      // refill: x stage kt + D goes to the slot of stage kt - 1, which every
+      // wave finished reading before this step's barrier
+      const int kn = kt + D < KT ? kt + D : KT - 1;
+      issue_x(kt + D, kn);
+      issue_w(kn, wr[u]);
+    }
+  }
+
+  // ---- epilogue: the fp32 tile through LDS (KS = 2: the second K half's
+  // partial tile first, then the first half's added onto it)
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  float* tile = reinterpret_cast<float*>(lds);
+  auto put = [&](bool add) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int col = wg * WE + j * 16 + fr;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float* p = tile + (i * 16 + fc * 4 + r) * TILE_LD + col;
+          *p = add ? acc[i][j][r] + *p : acc[i][j][r];
+        }
+      }
+  };
+  if constexpr (KS == 1) {
+    put(false);
+  } else {
+    if (kw == 1) put(false);
+    __syncthreads();
+    if (kw == 0) put(true);
+  }
+  __syncthreads();
+
+  // ---- scoring: G = E/V lanes per token
+  constexpr int G = E / V;
+  constexpr int TPP = NT / G;  // tokens per pass
+  __shared__ int hist[E];
+  if (counts) {
+    for (int i = threadIdx.x; i < E; i += NT) hist[i] = 0;
+    __syncthreads();
+  }
+  const int gl = threadIdx.x % G;
+  const int e0 = gl * V;
+  float bl[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) bl[j] = bias ? bias[e0 + j] : 0.0f;
+  const int k = KK > 0 ? KK : k_rt;
+  for (int tl = threadIdx.x / G; tl < BM; tl += TPP) {
+    const long long t = m0 + tl;
+    const float* row = tile + tl * TILE_LD;
+    float l[V];
+#pragma unroll
+    for (int j = 0; j < V; j += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(row + e0 + j);
+      l[j] = v[0]; l[j + 1] = v[1]; l[j + 2] = v[2]; l[j + 3] = v[3];
+    }
+    const bool valid = t < T;
+    if (valid) {
+#pragma unroll
+      for (int j = 0; j < V; j += 4)
+        *reinterpret_cast<f32x4*>(logits + t * E + e0 + j) =
+            (f32x4){l[j], l[j + 1], l[j + 2], l[j + 3]};
+    }
+    int my_id;
+    float wv;
+    score_token<E, V, KK, SC>(l, bl, row, 1, valid, gl, k_rt, renorm, n_group, topk_group,
+                              route_scale, norm_min, my_id, wv);
+    if (valid && gl < k) {
+      ids[t * k + gl] = my_id;
+      wout[t * k + gl] = wv;
+      if (counts) atomicAdd(&hist[my_id], 1);
+    }
+  }
+  if (counts) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < E; i += NT) {
+      const int c = hist[i];
+      if (c) atomicAdd(counts + i, c);
+    }
+  }
+}
+
+// Router weight [256, H] bf16 -> fragment-major copy: fragment f = (kt*2 + kk)*16 + g
+// holds, for lane l, the 8 values w[g*16 + (l & 15)][kt*64 + kk*32 + (l >> 4)*8 ..],
+// so each MFMA B fragment the GEMM loads is 1 KB contiguous.
+__global__ __launch_bounds__(256) void rf_wfrag_kernel(const u32x4* __restrict__ w, int H,
+                                                        u32x4* __restrict__ wf, int n) {
+  const int v = blockIdx.x * 256 + threadIdx.x;
+  if (v >= n) return;
+  const int l = v & 63, f = v >> 6;
+  const int g = f & 15, kk = (f >> 4) & 1, kt = f >> 5;
+  const int e = g * 16 + (l & 15);
+  const int k = kt * 64 + kk * 32 + (l >> 4) * 8;
+  wf[v] = w[((long long)e * H + k) / 8];
+}
+
+__global__ void rf_zero_kernel(int* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// The configuration shipped: 8 waves (two per SIMD) of 32 experts each, one
+// K half each per 32-wide K step pair, weights D = 4 steps ahead, the K loop
+// fully unrolled for H = 7168 (112 steps; the DeepSeek-V3 router).  A runtime
+// trip count makes the compiler merge its load bookkeeping at the loop head
+// into a vmcnt(0) that drains every load in flight once per iteration.
+constexpr int kRfWaves = 8, kRfKSplit = 1, kRfDepth = 4, kRfSteps = 112;
+
+bool route_fused_supported(int E, int H, int scoring, int n_group) {
+  return E == 256 && H == kRfSteps * rf::BK && topk_lane_width(E, scoring, n_group) == 16;
+}
+
+size_t route_fused_workspace_bytes(int H) { return (size_t)rf::E * H * 2; }
+
+template <int V, int KK, int SC>
+static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias, int T, int H,
+                            int k, int renorm, int n_group, int topk_group, float route_scale,
+                            float norm_min, float* logits, int32_t* ids, float* wout,
+                            int32_t* counts, hipStream_t s) {
+  constexpr int lds = route_fused_lds(kRfDepth);
+  auto kern = route_fused_kernel<kRfWaves, kRfKSplit, kRfDepth, kRfSteps, V, KK, SC>;
+  static bool attr = false;  // the attribute is per kernel; setting it twice is harmless
+  if (!attr) {
+    const hipError_t e =
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)((T + rf::BM - 1) / rf::BM)), dim3(64 * kRfWaves), lds,
+                     s, x, wf, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min,
+                     logits, ids, wout, counts);
+  return hipGetLastError();
+}
+
+// x [T, H] bf16, w [256, H] bf16; ws: route_fused_workspace_bytes(H) bytes
+// (the fragment-major weight copy).  Caller checked route_fused_supported.
+hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
+                              int k, int scoring, int renorm, int n_group, int topk_group,
+                              float route_scale, float norm_min, float* logits, int32_t* ids,
+                              float* wout, int32_t* counts, void* ws, hipStream_t s) {
+  if (counts) {
+    hipLaunchKernelGGL(rf_zero_kernel, dim3(1), dim3(256), 0, s, counts, 256);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (T == 0) return hipSuccess;
+  __bf16* wf = (__bf16*)ws;
+  {
+    const int n = rf::E * H / 8;
+    hipLaunchKernelGGL(rf_wfrag_kernel, dim3((n + 255) / 256), dim3(256), 0, s, (const u32x4*)w,
+                       H, (u32x4*)wf, n);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+#define MOE_RF_ARGS x, wf, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, \
+                    logits, ids, wout, counts, s
+#define MOE_RF_SC(SCV)                                       \
+  {                                                          \
+    if (k == 8) return launch_rf<16, 8, SCV>(MOE_RF_ARGS);   \
+    return launch_rf<16, 0, SCV>(MOE_RF_ARGS);               \
+  }
+  if (scoring == kScoreSoftmax) MOE_RF_SC(kScoreSoftmax)
+  if (scoring == kScoreSigmoidGroup) MOE_RF_SC(kScoreSigmoidGroup)
+  MOE_RF_SC(kScoreSoftmaxBias)
+#undef MOE_RF_SC
+#undef MOE_RF_ARGS
+}
+
+}  // namespace moe

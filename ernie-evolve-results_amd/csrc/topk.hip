@@ -17,102 +17,9 @@
 // The histogram is an LDS atomic per selected pair, flushed with one global
 // atomic per expert per block (K:1912-1919).  Integer atomics commute, so the
 // counts are deterministic.
-#include "moe_common.h"
-#include "moe_math.h"
+#include "score_token.h"
 
 namespace moe {
-
-constexpr int kScoreSoftmax = 0, kScoreSigmoidGroup = 1, kScoreSoftmaxBias = 2;
-
-// Partner value at butterfly level `lvl` inside aligned groups of 2^(lvl+1)
-// lanes.  Levels 0-3 are DPP moves (quad_perm xor1, xor2; row_half_mirror;
-// row_mirror) -- a mirror pairs lane i with the lane holding the other half
-// of its 2^(lvl+1) block, exactly like an xor, so pairwise sums keep the
-// adjacent-pair tree order.  Levels 4-5 cross DPP rows: xor shuffle.
-template <int LVL>
-__device__ __forceinline__ int partner_i(int v) {
-  if constexpr (LVL == 0) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
-  else if constexpr (LVL == 1) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
-  else if constexpr (LVL == 2) return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
-  else if constexpr (LVL == 3) return __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
-  else return __shfl_xor(v, 1 << LVL, 64);
-}
-template <int LVL>
-__device__ __forceinline__ float partner_f(float v) {
-  return __int_as_float(partner_i<LVL>(__float_as_int(v)));
-}
-
-// Runtime level -> compile-time partner (levels are uniform across the wave).
-#define MOE_FOR_LEVELS(LO, HI, ...)                                     \
-  {                                                                     \
-    if (0 >= (LO) && 0 < (HI)) { constexpr int L_ = 0; __VA_ARGS__ }   \
-    if (1 >= (LO) && 1 < (HI)) { constexpr int L_ = 1; __VA_ARGS__ }   \
-    if (2 >= (LO) && 2 < (HI)) { constexpr int L_ = 2; __VA_ARGS__ }   \
-    if (3 >= (LO) && 3 < (HI)) { constexpr int L_ = 3; __VA_ARGS__ }   \
-    if (4 >= (LO) && 4 < (HI)) { constexpr int L_ = 4; __VA_ARGS__ }   \
-    if (5 >= (LO) && 5 < (HI)) { constexpr int L_ = 5; __VA_ARGS__ }   \
-  }
-
-template <int V>
-__device__ __forceinline__ float local_pairwise_sum(const float (&e)[V]) {
-#pragma clang fp contract(off)
-  float s[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) s[j] = e[j];
-#pragma unroll
-  for (int w = V; w > 1; w >>= 1)
-#pragma unroll
-    for (int j = 0; j < w / 2; ++j) s[j] = s[2 * j] + s[2 * j + 1];
-  return s[0];
-}
-
-// Largest of V values (a max tree: independent ops, not one dependent
-// chain) and the lowest index holding it (a scan from the top, so ties keep
-// the lower index).
-template <int V>
-__device__ __forceinline__ void local_argmax(const float (&v)[V], int e0, float& bv, int& bi) {
-  float m[V];
-#pragma unroll
-  for (int j = 0; j < V; ++j) m[j] = v[j];
-#pragma unroll
-  for (int w = V; w > 1; w >>= 1)
-#pragma unroll
-    for (int j = 0; j < w / 2; ++j) m[j] = fmaxf(m[2 * j], m[2 * j + 1]);
-  bv = m[0];
-  int ix = V - 1;
-#pragma unroll
-  for (int j = V - 2; j >= 0; --j) ix = v[j] == bv ? j : ix;
-  bi = e0 + ix;
-}
-
-constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
-
-// V contiguous floats; 16-byte accesses when V is a multiple of 4 (a lane's
-// first expert is V-aligned and rows are E floats, so they are aligned).
-template <int V>
-__device__ __forceinline__ void load_vec(const float* __restrict__ p, float (&v)[V]) {
-  if constexpr (V % 4 == 0) {
-#pragma unroll
-    for (int j = 0; j < V; j += 4) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(p + j);
-      v[j] = a[0]; v[j + 1] = a[1]; v[j + 2] = a[2]; v[j + 3] = a[3];
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < V; ++j) v[j] = p[j];
-  }
-}
-template <int V>
-__device__ __forceinline__ void store_vec(float* __restrict__ p, const float (&v)[V]) {
-  if constexpr (V % 4 == 0) {
-#pragma unroll
-    for (int j = 0; j < V; j += 4)
-      *reinterpret_cast<f32x4*>(p + j) = (f32x4){v[j], v[j + 1], v[j + 2], v[j + 3]};
-  } else {
-#pragma unroll
-    for (int j = 0; j < V; ++j) p[j] = v[j];
-  }
-}
 
 // One token per G = E/V lanes; V contiguous experts per lane; 256 threads,
 // one pass: 4 * 64/G tokens per block.
@@ -124,10 +31,8 @@ __global__ __launch_bounds__(256) void topk_kernel(
     int* __restrict__ counts) {
 #pragma clang fp contract(off)
   constexpr int G = E / V;
-  constexpr int LG = ilog2c(G);
   constexpr int TPB = 4 * (64 / G);
   static_assert(G >= 8 && G <= 64 && V >= 1 && V <= 16, "lane shape");
-  constexpr float NEG_INF = -__builtin_inff();
   const int k = KK > 0 ? KK : k_rt;  // compile-time for the common k: the rounds unroll
   __shared__ int hist[E];
   const int tid = threadIdx.x;
@@ -164,146 +69,13 @@ __global__ __launch_bounds__(256) void topk_kernel(
   float b[V];
 #pragma unroll
   for (int j = 0; j < V; ++j) b[j] = bias ? bias[e0 + j] : 0.0f;
-
-  // ---- scores: sel (what is ranked) and aux (what the weight is made of)
-  float sel[V];
-  float fullsum = 1.0f;
-  if constexpr (SC == kScoreSoftmax) {
-#pragma unroll
-    for (int j = 0; j < V; ++j) sel[j] = l[j] + b[j];
-    if (!renorm) {
-      float m = sel[0];
-#pragma unroll
-      for (int j = 1; j < V; ++j) m = fmaxf(m, sel[j]);
-      MOE_FOR_LEVELS(0, LG, { m = fmaxf(m, partner_f<L_>(m)); })
-      float e[V];
-#pragma unroll
-      for (int j = 0; j < V; ++j) e[j] = det_exp(sel[j] - m);
-      float sum = local_pairwise_sum<V>(e);
-      MOE_FOR_LEVELS(0, LG, { sum = sum + partner_f<L_>(sum); })
-      fullsum = sum;
-    }
-  } else if constexpr (SC == kScoreSoftmaxBias) {
-    // K:1857-1866: e = exp(l - max), p = e * (1/sum), c = p + bias
-    float m = l[0];
-#pragma unroll
-    for (int j = 1; j < V; ++j) m = fmaxf(m, l[j]);
-    MOE_FOR_LEVELS(0, LG, { m = fmaxf(m, partner_f<L_>(m)); })
-    float e[V];
-#pragma unroll
-    for (int j = 0; j < V; ++j) e[j] = det_exp(l[j] - m);
-    float sum = local_pairwise_sum<V>(e);
-    MOE_FOR_LEVELS(0, LG, { sum = sum + partner_f<L_>(sum); })
-    const float rs = __fdiv_rn(1.0f, sum);
-#pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const float p = e[j] * rs;
-      sel[j] = p + b[j];
-    }
-  } else {  // sigmoid + selection bias, group-limited
-#pragma unroll
-    for (int j = 0; j < V; ++j) sel[j] = det_sigmoid(l[j]) + b[j];
-    if (n_group > 1) {
-      const int lgl = ilog2c((E / n_group) / V);  // log2(lanes per group), V divides the group
-      float t1 = NEG_INF, t2 = NEG_INF;
-#pragma unroll
-      for (int j = 0; j < V; ++j) {
-        // running top two, as selects: (t1, t2) <- top2(t1, t2, v)
-        t2 = fmaxf(t2, fminf(t1, sel[j]));
-        t1 = fmaxf(t1, sel[j]);
-      }
-      MOE_FOR_LEVELS(0, lgl, {
-        const float o1 = partner_f<L_>(t1), o2 = partner_f<L_>(t2);
-        const float n1 = fmaxf(t1, o1);
-        const float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
-        t1 = n1;
-        t2 = n2;
-      })
-      const float gscore = t1 + t2;
-      const int g = gl >> lgl;
-      bool kept = false;
-      for (int r = 0; r < topk_group; ++r) {
-        float bv = kept ? NEG_INF : gscore;
-        int bg = g;
-        MOE_FOR_LEVELS(lgl, LG, {
-          const float ov = partner_f<L_>(bv);
-          const int og = partner_i<L_>(bg);
-          const bool take = (ov > bv) | ((ov == bv) & (og < bg));
-          bv = take ? ov : bv;
-          bg = take ? og : bg;
-        })
-        if (bg == g) kept = true;
-      }
-      if (!kept) {
-#pragma unroll
-        for (int j = 0; j < V; ++j) sel[j] = NEG_INF;
-      }
-    }
-  }
-
-  // ---- k rounds of group argmax (ties -> lower index, K:1886).  Only the
-  // ranked value and its index travel; the sigmoid weight of a winner is
-  // recomputed from its logit afterwards (same operations, same bits).
-  int my_id = 0;
-  float my_sel = 0.0f, m0 = 0.0f;
-  float acc = 0.0f;  // sequential slot-order sum the weights divide by
-#pragma unroll
-  for (int r = 0; r < (KK > 0 ? KK : 8); ++r) {
-    if (KK == 0 && r >= k) break;
-    float bv;
-    int bi;
-    local_argmax<V>(sel, e0, bv, bi);
-    MOE_FOR_LEVELS(0, LG, {
-      const float ov = partner_f<L_>(bv);
-      const int oi = partner_i<L_>(bi);
-      // non-short-circuit: a select, not a branch
-      const bool take = (ov > bv) | ((ov == bv) & (oi < bi));
-      bv = take ? ov : bv;
-      bi = take ? oi : bi;
-    })
-    if (gl == r) { my_id = bi; my_sel = bv; }
-#pragma unroll
-    for (int j = 0; j < V; ++j)
-      if (e0 + j == bi) sel[j] = NEG_INF;
-    if constexpr (SC == kScoreSoftmax) {
-      if (r == 0) m0 = bv;
-      const float e = det_exp(bv - m0);
-      acc = (r == 0) ? e : acc + e;
-    } else if constexpr (SC == kScoreSoftmaxBias) {
-      acc = (r == 0) ? bv : acc + bv;
-    }
-  }
-  if constexpr (SC == kScoreSigmoidGroup) {
-    // a slot's weight is the sigmoid of its expert's logit; the divisor is
-    // the sequential slot-order sum of those, read lane by lane from the
-    // token's first k lanes
-    float my_aux = 0.0f;
-    if (valid && gl < k) {
-      const float* src = logits + t * (long long)(nparts * E) + my_id;
-      float lv = src[0];
-      for (int p = 1; p < nparts; ++p) lv = lv + src[p * E];
-      my_aux = det_sigmoid(lv);
-    }
-    const int base = (threadIdx.x & 63) - gl;
-    for (int r = 0; r < k; ++r) {
-      const float a = __shfl(my_aux, base + r, 64);
-      acc = (r == 0) ? a : acc + a;
-    }
-    my_sel = my_aux;  // the weight numerator below
-  }
-
-  // lane gl < k holds slot gl (G >= 8 >= k)
+  int my_id;
+  float wv;
+  score_token<E, V, KK, SC>(l, b, logits + (valid ? t : 0) * (long long)(nparts * E), nparts,
+                            valid, gl, k_rt, renorm, n_group, topk_group, route_scale, norm_min,
+                            my_id, wv);
   {
     if (valid && gl < k) {
-      float wv;
-      if constexpr (SC == kScoreSoftmax) {
-        const float e = det_exp(my_sel - m0);
-        wv = __fdiv_rn(e, renorm ? acc : fullsum) * route_scale;
-      } else if constexpr (SC == kScoreSigmoidGroup) {
-        wv = (renorm ? __fdiv_rn(my_sel, acc + 1e-20f) : my_sel) * route_scale;
-      } else {
-        wv = __fdiv_rn(my_sel, fmaxf(acc, norm_min));  // K:1909
-      }
       ids[t * k + gl] = my_id;
       wout[t * k + gl] = wv;
       if (counts) atomicAdd(&hist[my_id], 1);

@@ -79,7 +79,10 @@ const char* moe_last_error_string(void);
  *     weights (hi and lo halves) or a K split (ksplit > 1, chosen when the
  *     row x expert tiles alone leave the chip's 256 CUs idle, e.g. small T):
  *     [T, parts*E] fp32 partial sums.
- * The DeepSeek-V3 shape with bf16 weights (T=32768, H=7168, E=256) needs 0. */
+ *   - E = 256, H = 7168 with bf16 weights: the router GEMM and the scoring run
+ *     as one kernel that reads a fragment-major copy of the weight, E*H*2
+ *     bytes (3.5 MiB), rewritten by every call.
+ * The size does not depend on cfg; it covers whichever path the call takes. */
 size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype);
 
 /* Stage 1: router GEMM, logits[T,E] fp32 = x[T,H] bf16 . w[E,H]^T bf16, fp32

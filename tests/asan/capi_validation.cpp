@@ -55,8 +55,8 @@ int main() {
   EXPECT(moe_quant_rows_i8(fake, 6, 256, 16, 1.0f, 4, ip, (int8_t*)fake, fp, nullptr), MOE_ERR_INVALID_ARG);
   EXPECT(moe_quant_rows_i8(nullptr, 0, 256, 0, 1.0f, 0, nullptr, nullptr, nullptr, nullptr), MOE_OK);
   if (moe_grouped_gemm_workspace_bytes(64) != 512) ++failures;
-  // C4 bf16: 128 x 2 GEMM tiles fill the chip without a K split -> no workspace
-  if (moe_route_workspace_bytes(32768, 7168, 256, MOE_DTYPE_BF16) != 0) ++failures;
+  // C4 bf16: the fused GEMM + scoring kernel's fragment-major weight copy [256, 7168] bf16
+  if (moe_route_workspace_bytes(32768, 7168, 256, MOE_DTYPE_BF16) != (size_t)256 * 7168 * 2) ++failures;
   // fp32 weights: [2E,H] bf16 hi/lo split + [T,2E] fp32 hi/lo partial logits
   if (moe_route_workspace_bytes(32768, 7168, 256, MOE_DTYPE_FP32) != (size_t)2 * 256 * 7168 * 2 + (size_t)32768 * 512 * 4) ++failures;
   if (moe_permute_workspace_bytes(32768, 256, 8) != (size_t)256 * 1024 * 4 + 1024) ++failures;

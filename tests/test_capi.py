@@ -121,7 +121,10 @@ def _route_ws(T, H, E, fp32):
     N = 2 * E if fp32 else E
     parts = (N // E) * _router_ksplit(T, H, N)
     b = r256(2 * E * H * 2) if fp32 else 0
-    return b + (r256(T * parts * E * 4) if parts > 1 else 0)
+    b += r256(T * parts * E * 4) if parts > 1 else 0
+    if not fp32 and E == 256 and H == 7168:  # fused GEMM + scoring: fragment-major weight copy
+        b = max(b, r256(E * H * 2))
+    return b
 
 
 def test_workspace_sizes():
@@ -132,11 +135,13 @@ def test_workspace_sizes():
     # fp32 weights: [2E,H] bf16 split (4096 B) + [T, 2 halves * 2 K parts * E] fp32
     assert L.moe_route_workspace_bytes(100, 128, 8, 1) == 4096 + 12800
     assert L.moe_route_workspace_bytes(100, 64, 8, 0) == 0        # H=64: one K step, no split
-    # DeepSeek-V3 shape: 128 row tiles x 2 expert tiles fill the chip, no split, no workspace
-    assert L.moe_route_workspace_bytes(32768, 7168, 256, 0) == 0
+    # DeepSeek-V3 shape: the fused GEMM + scoring kernel keeps a fragment-major copy of the
+    # [256, 7168] bf16 weight
+    assert L.moe_route_workspace_bytes(32768, 7168, 256, 0) == 256 * 7168 * 2
     # ... but fp32 weights there still need the [2E,H] split and [T, 2E] hi/lo partial logits
     assert L.moe_route_workspace_bytes(32768, 7168, 256, 1) == 2 * 256 * 7168 * 2 + 32768 * 512 * 4
-    assert L.moe_route_workspace_bytes(65536, 7168, 256, 0) == 0
+    assert L.moe_route_workspace_bytes(65536, 7168, 256, 0) == 256 * 7168 * 2
+    assert L.moe_route_workspace_bytes(32768, 4096, 256, 0) == 0   # no fused kernel, no K split
     for T, H, E in [(1, 64, 8), (100, 128, 8), (512, 1024, 8), (8192, 4096, 8), (16384, 2048, 128),
                     (1571, 8192, 64), (32768, 7168, 256), (300, 7168, 256), (4096, 8192, 64)]:
         for fp32 in (0, 1):
