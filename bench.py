@@ -51,8 +51,7 @@ def algorithmic_bytes(c):
     route = T * H * xb + E * H * wb + T * E * 4 + T * k * 8
     gather = T * H * xb + T * k * H * db + (T * k * (H // 128) * 4 if c.fp8 else 0) + T * k * 8
     combine = T * k * H * 2 + T * H * 2 + T * k * 8
-    return dict(route=route, gather=gather, combine=combine, router_gemm=T * H * xb + E * H * wb
-                + T * E * 4)
+    return dict(route=route, gather=gather, combine=combine)
 
 
 TRAFFIC_FILES = {"C4": "c4_hbm_traffic.md", "C5": "c5_fp8_dispatch_hbm_traffic.md"}
@@ -183,7 +182,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="C4")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=16384)
+    ap.add_argument("--cpu-tokens", type=int, default=0,
+                    help="tokens of the CPU baseline sample (0: the whole configuration)")
     ap.add_argument("--cpu-threads", type=int, default=0,
                     help="threads for the CPU baseline (0: every core of this process)")
     ap.add_argument("--copy-calib", action="store_true",
@@ -238,13 +238,13 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
 
     # ---- per-stage HIP-event timing (on the stream the kernels run on).
-    # permute = 3 index kernels + the gather launch; an index-only permute
-    # (no rows) isolates the gather.  route = GEMM + scoring; a standalone
-    # scoring launch on the finished logits isolates the GEMM.
+    # permute = index kernels + the gather launch; an index-only permute (no
+    # rows) isolates the gather.  route = the router GEMM and the scoring (one
+    # fused kernel at the DeepSeek-V3 shape, plus its weight re-layout pass).
     ev = lambda: torch.cuda.Event(enable_timing=True)
-    st = {"route": [], "permute": [], "permute_index": [], "combine": [], "topk": []}
+    st = {"route": [], "permute": [], "permute_index": [], "combine": []}
     for _ in range(args.steps):
-        e = [ev() for _ in range(6)]
+        e = [ev() for _ in range(5)]
         e[0].record()
         plan.route(x, w, bias)
         e[1].record()
@@ -254,14 +254,11 @@ def main():
         e[3].record()
         plan.permute(x, index_only=True)
         e[4].record()
-        plan.topk_only(bias)
-        e[5].record()
         torch.cuda.synchronize()
         st["route"].append(e[0].elapsed_time(e[1]) * 1e3)
         st["permute"].append(e[1].elapsed_time(e[2]) * 1e3)
         st["combine"].append(e[2].elapsed_time(e[3]) * 1e3)
         st["permute_index"].append(e[3].elapsed_time(e[4]) * 1e3)
-        st["topk"].append(e[4].elapsed_time(e[5]) * 1e3)
     us = {k2: statistics.mean(v) for k2, v in st.items()}
 
     # ---- cold-cache step: 20 single steps, each after a 1 GiB rewrite that
@@ -279,7 +276,6 @@ def main():
     del flush
     cold_ms = statistics.median(cold)
     us["gather"] = us["permute"] - us["permute_index"]
-    us["router_gemm"] = max(us["route"] - us["topk"], 1e-3)
 
     ab = algorithmic_bytes(c)
     traffic = measured_traffic(c.name)
@@ -296,14 +292,15 @@ def main():
     total_bytes = ab["route"] + ab["gather"] + ab["combine"]
     e2e_gbs = total_bytes / (ms_per_step * 1e-3) / 1e9
     flops = 2.0 * c.T * c.H * c.E
-    gemm = {"us": round(us["router_gemm"], 2),
-            "tflops": round(flops / (us["router_gemm"] * 1e-6) / 1e12, 1),
-            "mfma_frac": round(flops / (us["router_gemm"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
-            "hbm_frac": round(ab["router_gemm"] / (us["router_gemm"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    # the router stage as a whole (GEMM + scoring): MFMA and HBM fractions
+    route = {"us": round(us["route"], 2),
+             "tflops": round(flops / (us["route"] * 1e-6) / 1e12, 1),
+             "mfma_frac": round(flops / (us["route"] * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
+             "hbm_frac": round(ab["route"] / (us["route"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(c, args.cpu_tokens, args.cpu_threads)
+        cpu = cpu_baseline(c, args.cpu_tokens or c.T, args.cpu_threads)
 
     tok_s = c.T / (ms_per_step * 1e-3)
     line = {
@@ -325,7 +322,7 @@ def main():
             "permute": round(ab["gather"] / (us["permute"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "gather": round(ab["gather"] / (us["gather"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "combine": round(ab["combine"] / (us["combine"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
-        "router_gemm": gemm,
+        "route_mfma": route,
         "cold_step": {"ms": round(cold_ms, 4), "tokens_per_s": round(c.T / (cold_ms * 1e-3), 1),
                       "note": "median of 20 single steps, each after a 1 GiB rewrite (L2 + MALL)"},
         "cpu_baseline": cpu,

@@ -36,12 +36,13 @@ def test_algorithmic_bytes_match_the_scope_table(name, total_gb, route_gb, dispa
     assert total / 1e9 == pytest.approx(total_gb, abs=0.001)
 
 
-def test_router_gemm_bytes_count_an_fp32_weight_whole():
+def test_route_bytes_count_an_fp32_weight_whole():
     """C1's router weight is fp32 (split into bf16 hi/lo on the device): its
     E*H*4 bytes are read, twice the bf16 weight's."""
     c1 = CONFIGS["C1"]
     ab = bench.algorithmic_bytes(c1)
-    assert ab["router_gemm"] == c1.T * c1.H * 2 + c1.E * c1.H * 4 + c1.T * c1.E * 4
+    assert ab["route"] == (c1.T * c1.H * 2 + c1.E * c1.H * 4 + c1.T * c1.E * 4
+                           + c1.T * c1.k * 8)
 
 
 def test_more_than_one_gpu_is_refused():
