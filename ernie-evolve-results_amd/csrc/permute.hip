@@ -9,10 +9,11 @@
 // ordinary (temporal) loads, which hit the part of x the router GEMM left in
 // the memory-side cache (MALL); the k rows are written non-temporal.
 //
-// fp8 variant (the reference has no routed fp8 permute): a 16-lane group owns
-// one 1x128 block of a token row (8 bf16 per lane), reduces |x| max over the
+// fp8 variant (the reference has no routed fp8 permute): an 8-lane group owns
+// one 1x128 block of a token row (16 bf16 per lane), reduces |x| max over the
 // group with xor shuffles, and writes e4m3fn(clamp(x / s, +-448)) with
-// s = max(amax, 1e-10) / 448 into all k rows, plus the scale.
+// s = max(amax, 1e-10) / 448 into all k rows (16 bytes per lane), plus the
+// scale.
 #include "moe_common.h"
 
 namespace moe {
@@ -70,56 +71,63 @@ __device__ __forceinline__ unsigned int cvt_fp8x4(float a, float b, float c, flo
   return (unsigned int)w;
 }
 
+// One lane per 16 consecutive elements (two 16-byte loads, one 16-byte e4m3fn
+// store per destination row); the 8 lanes of a 1x128 block reduce |x| max
+// with xor shuffles, and the block's first lane writes the scale -- the 8
+// blocks of a wavefront's 1 KB of fp8 row land as 8 consecutive scales, one
+// 32-byte run per store instruction.
 __global__ __launch_bounds__(256) void gather_fp8_kernel(const u32x4* __restrict__ x,
                                                          const int* __restrict__ pair_row,
-                                                         int ngroups, int nb, int H, int k,
-                                                         unsigned char* __restrict__ xg,
+                                                         long long nchunks, int cpr, int nb,
+                                                         int k, u32x4* __restrict__ xg,
                                                          float* __restrict__ scales) {
-  // One 16-lane group per (token, 128-block).  The 16 lanes of a group share
-  // g, so they enter and leave the loop together and the xor shuffles below
-  // only read lanes of their own group.
-  const int lane16 = threadIdx.x & 15;
-  for (int g = (blockIdx.x * 256 + threadIdx.x) >> 4; g < ngroups; g += gridDim.x * 16) {
-    const int t = g / nb;
-    const int blk = g - t * nb;
-    const u32x4 raw = x[((long long)t * H + blk * 128) / 8 + lane16];
-    float f[8];
+  // chunk c = t * cpr + v: 16 elements of token t; cpr = H / 16 is a multiple
+  // of 8, so the 8 lanes of a block share t and leave the loop together
+  const int lane8 = threadIdx.x & 7;
+  for (long long c = (long long)blockIdx.x * 256 + threadIdx.x; c < nchunks;
+       c += (long long)gridDim.x * 256) {
+    const int t = (int)(c / cpr);
+    const int v = (int)(c - (long long)t * cpr);
+    const u32x4 r0 = x[2 * c], r1 = x[2 * c + 1];
+    float f[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      f[2 * q] = bf16lo(raw[q]);
-      f[2 * q + 1] = bf16hi(raw[q]);
+      f[2 * q] = bf16lo(r0[q]);
+      f[2 * q + 1] = bf16hi(r0[q]);
+      f[8 + 2 * q] = bf16lo(r1[q]);
+      f[8 + 2 * q + 1] = bf16hi(r1[q]);
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(f[q]));
+    for (int q = 0; q < 16; ++q) amax = fmaxf(amax, fabsf(f[q]));
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
     const float scale = __fdiv_rn(fmaxf(amax, 1e-10f), 448.0f);
-    float qv[8];
+    float qv[16];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) qv[q] = fminf(fmaxf(__fdiv_rn(f[q], scale), -448.0f), 448.0f);
-    u32x2 packed;
-    packed[0] = cvt_fp8x4(qv[0], qv[1], qv[2], qv[3]);
-    packed[1] = cvt_fp8x4(qv[4], qv[5], qv[6], qv[7]);
+    for (int q = 0; q < 16; ++q) qv[q] = fminf(fmaxf(__fdiv_rn(f[q], scale), -448.0f), 448.0f);
+    u32x4 packed;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      packed[q] = cvt_fp8x4(qv[4 * q], qv[4 * q + 1], qv[4 * q + 2], qv[4 * q + 3]);
     const int* pr = pair_row + (long long)t * k;
+    const int blk = v >> 3;
     for (int j = 0; j < k; ++j) {
       const int r = pr[j];
       if (r < 0) continue;
-      u32x2* dst = reinterpret_cast<u32x2*>(xg + (long long)r * H + blk * 128) + lane16;
-      __builtin_nontemporal_store(packed, dst);
-      if (lane16 == 0) scales[(long long)r * nb + blk] = scale;
+      st_nt(xg + (long long)r * cpr + v, packed);
+      if (lane8 == 0) scales[(long long)r * nb + blk] = scale;
     }
   }
 }
 
 hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, int T, int H, int k,
                              void* xg, float* scales, hipStream_t s) {
-  const int nb = H / 128;
-  const int ngroups = T * nb;
-  if (ngroups == 0) return hipSuccess;
-  const long long threads = (long long)ngroups * 16;
-  hipLaunchKernelGGL(gather_fp8_kernel, dim3(grid_for(threads)), dim3(256), 0, s,
-                     (const u32x4*)x, pair_row, ngroups, nb, H, k, (unsigned char*)xg, scales);
+  const int cpr = H / 16;  // 16-element chunks per row (H % 128 == 0: a multiple of 8)
+  const long long nchunks = (long long)T * cpr;
+  if (nchunks == 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_fp8_kernel, dim3(grid_for(nchunks)), dim3(256), 0, s,
+                     (const u32x4*)x, pair_row, nchunks, cpr, H / 128, k, (u32x4*)xg, scales);
   return hipGetLastError();
 }
 
