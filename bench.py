@@ -175,6 +175,72 @@ def layer_bench(Ts, steps, warmup, dispatch="bf16", experts="bf16", cold=True):
     print(json.dumps(line), flush=True)
 
 
+def ceiling_bench(c, dev, reps):
+    """The machine's rate for each stage's byte mix at this configuration's
+    sizes: moe_stream_probe kernels (sequential addresses, the stage's cache
+    policy) timed beside the real stages on the same buffers, both back to
+    back (as in the step) and each after a 1 GiB rewrite.  Prints one JSON
+    line."""
+    x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
+    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, dev, fp8=c.fp8)
+    L = M.lib()
+    stream = M._stream(x)
+    nx = c.T * c.H * 2 // 16            # 16-byte vectors of x (and of out)
+    P = M._ptr
+    # 1 GiB rewrite as 4 streams (its own kernel symbol, apart from the probes)
+    flush = lambda: L.moe_stream_probe(1, None, P(plan.xg), (1 << 30) // 16 // 4, 4, stream)
+    pats = {  # name: (pattern, src, dst, nvec, ways, bytes read, bytes written)
+        "x_read": (0, x, plan.out, nx, 1, nx * 16, 0),
+        "rows_read": (0, y, plan.out, nx, c.k, c.k * nx * 16, 0),
+        "rows_write": (1, None, plan.xg, nx, c.k, 0, c.k * nx * 16),
+        "gather_mix": (2, x, plan.xg, nx, c.k, nx * 16, c.k * nx * 16),
+        "combine_mix": (3, y, plan.out, nx, c.k, c.k * nx * 16, nx * 16),
+        "copy_1GiB": (4, y, plan.xg, (1 << 30) // 16, 1, 1 << 30, 1 << 30),
+    }
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def timed(f, cold):
+        ts = []
+        for _ in range(reps + 2):
+            if cold:
+                flush()
+            a, b = ev(), ev()
+            a.record()
+            f()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3)
+        return statistics.median(ts[2:])
+
+    out = {}
+    for name, (pat, src, dst, n, ways, rb, wb) in pats.items():
+        f = lambda: M._check(L.moe_stream_probe(pat, P(src), P(dst), n, ways, stream))
+        row = {"read_GB": round(rb / 1e9, 3), "write_GB": round(wb / 1e9, 3)}
+        for ctx in ("warm", "cold"):
+            us = timed(f, ctx == "cold")
+            row[ctx + "_us"] = round(us, 1)
+            row[ctx + "_TBps"] = round((rb + wb) / (us * 1e-6) / 1e12, 2)
+        out[name] = row
+    # the real stages on the same buffers (same two contexts)
+    plan.step(x, w, bias, y)
+    real = {"route": lambda: plan.route(x, w, bias), "gather": lambda: plan.permute(x),
+            "combine": lambda: plan.combine(y)}
+    ab = algorithmic_bytes(c)
+    rbytes = {"route": ab["route"], "gather": ab["gather"], "combine": ab["combine"]}
+    rr = {}
+    for name, f in real.items():
+        row = {"algorithmic_GB": round(rbytes[name] / 1e9, 3)}
+        for ctx in ("warm", "cold"):
+            us = timed(f, ctx == "cold")
+            row[ctx + "_us"] = round(us, 1)
+            row[ctx + "_TBps"] = round(rbytes[name] / (us * 1e-6) / 1e12, 2)
+        rr[name] = row
+    print(json.dumps({"mode": "ceiling", "config": c.name, "reps": reps,
+                      "note": "warm: back to back; cold: each after a 1 GiB rewrite. gather = "
+                              "moe_permute (index kernels + gather)",
+                      "probes": out, "real": rr}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +255,9 @@ def main():
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one plain 1 GiB device copy (untimed), the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="time plain streaming kernels that move each stage's byte mix "
+                         "(moe_stream_probe) beside the real stages, on the same buffers")
     ap.add_argument("--layer", nargs="*", type=int, default=None,
                     help="time run() at the reference's workload T values (default: its mix)")
     ap.add_argument("--layer-fp8", action="store_true",
@@ -211,6 +280,9 @@ def main():
 
     c = CONFIGS[args.config]
     dev = torch.device("cuda:0")
+    if args.ceiling:
+        ceiling_bench(c, dev, max(args.steps, 5))
+        return
     x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
     # The router takes bf16 hidden states (K:4327-4339); an fp32 config (C1)
     # hands the GPU path bf16(x), cast once here, and keeps its fp32 router

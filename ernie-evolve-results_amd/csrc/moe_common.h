@@ -91,6 +91,10 @@ hipError_t launch_quant_rows_i8(const __bf16* x, long long R, int K, int had, fl
                                 int group_rows, const int* counts, signed char* q, float* s,
                                 hipStream_t st);
 
+// Streaming probes of the stage byte mixes (pattern: MOE_PROBE_*).
+hipError_t launch_stream_probe(int pattern, const void* src, void* dst, long long nvec, int ways,
+                               hipStream_t s);
+
 // Experts per lane of the scoring kernel for (E, scoring, n_group).
 int topk_lane_width(int E, int scoring, int n_group);
 

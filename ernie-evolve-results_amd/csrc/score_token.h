@@ -104,19 +104,24 @@ __device__ __forceinline__ void store_vec(float* __restrict__ p, const float (&v
   }
 }
 
-// One token's scores, held by G = E/V consecutive lanes (lane gl of the token
-// owns experts [gl*V, gl*V + V)).  l: the lane's logits, b: their bias.  row:
-// the token's logit row (nparts partial blocks of E floats side by side, read
-// only to recompute a selected expert's sigmoid weight).  Lanes gl < k return
-// slot gl's expert in id_out and its weight in w_out.  Every lane of the
-// token's G must call it (cross-lane reductions); `valid` is false for a
-// padding token.
-template <int E, int V, int KK, int SC>
-__device__ __forceinline__ void score_token(const float (&l)[V], const float (&b)[V],
-                                            const float* row, int nparts, bool valid, int gl,
-                                            int k_rt, int renorm, int n_group, int topk_group,
-                                            float route_scale, float norm_min, int& id_out,
-                                            float& w_out) {
+// NT tokens' scores at once, each held by G = E/V consecutive lanes (lane gl
+// of a token owns experts [gl*V, gl*V + V)).  Token n: l[n] the lane's
+// logits, row[n] its logit row (nparts partial blocks of E floats side by
+// side, read only to recompute a selected expert's sigmoid weight), valid[n]
+// false for a padding token; b: the lane's bias.  Lanes gl < k return slot
+// gl's expert in id_out[n] and its weight in w_out[n].  Every lane of the
+// token's G must call it (cross-lane reductions).
+//
+// Each token gets exactly the operation sequence of a lone token (so the
+// result does not depend on NT); NT > 1 only interleaves independent
+// tokens' instructions, which hides the latency of the DPP / shuffle chains.
+template <int E, int V, int KK, int SC, int NT>
+__device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const float (&b)[V],
+                                             const float* const (&row)[NT], int nparts,
+                                             const bool (&valid)[NT], int gl, int k_rt,
+                                             int renorm, int n_group, int topk_group,
+                                             float route_scale, float norm_min,
+                                             int (&id_out)[NT], float (&w_out)[NT]) {
 #pragma clang fp contract(off)
   constexpr int G = E / V;
   constexpr int LG = ilog2c(G);
@@ -124,149 +129,238 @@ __device__ __forceinline__ void score_token(const float (&l)[V], const float (&b
   const int k = KK > 0 ? KK : k_rt;
   const int e0 = gl * V;
   // ---- scores: sel (what is ranked) and aux (what the weight is made of)
-  float sel[V];
-  float fullsum = 1.0f;
+  float sel[NT][V];
+  float fullsum[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) fullsum[n] = 1.0f;
   if constexpr (SC == kScoreSoftmax) {
 #pragma unroll
-    for (int j = 0; j < V; ++j) sel[j] = l[j] + b[j];
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int j = 0; j < V; ++j) sel[n][j] = l[n][j] + b[j];
     if (!renorm) {
-      float m = sel[0];
+      float m[NT], sum[NT];
 #pragma unroll
-      for (int j = 1; j < V; ++j) m = fmaxf(m, sel[j]);
-      MOE_FOR_LEVELS(0, LG, { m = fmaxf(m, partner_f<L_>(m)); })
-      float e[V];
+      for (int n = 0; n < NT; ++n) {
+        m[n] = sel[n][0];
 #pragma unroll
-      for (int j = 0; j < V; ++j) e[j] = det_exp(sel[j] - m);
-      float sum = local_pairwise_sum<V>(e);
-      MOE_FOR_LEVELS(0, LG, { sum = sum + partner_f<L_>(sum); })
-      fullsum = sum;
+        for (int j = 1; j < V; ++j) m[n] = fmaxf(m[n], sel[n][j]);
+      }
+      MOE_FOR_LEVELS(0, LG, {
+        for (int n = 0; n < NT; ++n) m[n] = fmaxf(m[n], partner_f<L_>(m[n]));
+      })
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        float e[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) e[j] = det_exp(sel[n][j] - m[n]);
+        sum[n] = local_pairwise_sum<V>(e);
+      }
+      MOE_FOR_LEVELS(0, LG, {
+        for (int n = 0; n < NT; ++n) sum[n] = sum[n] + partner_f<L_>(sum[n]);
+      })
+#pragma unroll
+      for (int n = 0; n < NT; ++n) fullsum[n] = sum[n];
     }
   } else if constexpr (SC == kScoreSoftmaxBias) {
     // K:1857-1866: e = exp(l - max), p = e * (1/sum), c = p + bias
-    float m = l[0];
+    float m[NT], sum[NT], e[NT][V];
 #pragma unroll
-    for (int j = 1; j < V; ++j) m = fmaxf(m, l[j]);
-    MOE_FOR_LEVELS(0, LG, { m = fmaxf(m, partner_f<L_>(m)); })
-    float e[V];
+    for (int n = 0; n < NT; ++n) {
+      m[n] = l[n][0];
 #pragma unroll
-    for (int j = 0; j < V; ++j) e[j] = det_exp(l[j] - m);
-    float sum = local_pairwise_sum<V>(e);
-    MOE_FOR_LEVELS(0, LG, { sum = sum + partner_f<L_>(sum); })
-    const float rs = __fdiv_rn(1.0f, sum);
+      for (int j = 1; j < V; ++j) m[n] = fmaxf(m[n], l[n][j]);
+    }
+    MOE_FOR_LEVELS(0, LG, {
+      for (int n = 0; n < NT; ++n) m[n] = fmaxf(m[n], partner_f<L_>(m[n]));
+    })
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      const float p = e[j] * rs;
-      sel[j] = p + b[j];
+    for (int n = 0; n < NT; ++n) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) e[n][j] = det_exp(l[n][j] - m[n]);
+      sum[n] = local_pairwise_sum<V>(e[n]);
+    }
+    MOE_FOR_LEVELS(0, LG, {
+      for (int n = 0; n < NT; ++n) sum[n] = sum[n] + partner_f<L_>(sum[n]);
+    })
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const float rs = __fdiv_rn(1.0f, sum[n]);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float p = e[n][j] * rs;
+        sel[n][j] = p + b[j];
+      }
     }
   } else {  // sigmoid + selection bias, group-limited
 #pragma unroll
-    for (int j = 0; j < V; ++j) sel[j] = det_sigmoid(l[j]) + b[j];
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int j = 0; j < V; ++j) sel[n][j] = det_sigmoid(l[n][j]) + b[j];
     if (n_group > 1) {
       const int lgl = ilog2c((E / n_group) / V);  // log2(lanes per group), V divides the group
-      float t1 = NEG_INF, t2 = NEG_INF;
+      float t1[NT], t2[NT], gscore[NT];
+      bool kept[NT];
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        // running top two, as selects: (t1, t2) <- top2(t1, t2, v)
-        t2 = fmaxf(t2, fminf(t1, sel[j]));
-        t1 = fmaxf(t1, sel[j]);
+      for (int n = 0; n < NT; ++n) {
+        t1[n] = NEG_INF;
+        t2[n] = NEG_INF;
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          // running top two, as selects: (t1, t2) <- top2(t1, t2, v)
+          t2[n] = fmaxf(t2[n], fminf(t1[n], sel[n][j]));
+          t1[n] = fmaxf(t1[n], sel[n][j]);
+        }
       }
       MOE_FOR_LEVELS(0, lgl, {
-        const float o1 = partner_f<L_>(t1), o2 = partner_f<L_>(t2);
-        const float n1 = fmaxf(t1, o1);
-        const float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
-        t1 = n1;
-        t2 = n2;
+        for (int n = 0; n < NT; ++n) {
+          const float o1 = partner_f<L_>(t1[n]), o2 = partner_f<L_>(t2[n]);
+          const float n1 = fmaxf(t1[n], o1);
+          const float n2 = fmaxf(fminf(t1[n], o1), fmaxf(t2[n], o2));
+          t1[n] = n1;
+          t2[n] = n2;
+        }
       })
-      const float gscore = t1 + t2;
       const int g = gl >> lgl;
-      bool kept = false;
-      for (int r = 0; r < topk_group; ++r) {
-        float bv = kept ? NEG_INF : gscore;
-        int bg = g;
-        MOE_FOR_LEVELS(lgl, LG, {
-          const float ov = partner_f<L_>(bv);
-          const int og = partner_i<L_>(bg);
-          const bool take = (ov > bv) | ((ov == bv) & (og < bg));
-          bv = take ? ov : bv;
-          bg = take ? og : bg;
-        })
-        if (bg == g) kept = true;
-      }
-      if (!kept) {
 #pragma unroll
-        for (int j = 0; j < V; ++j) sel[j] = NEG_INF;
+      for (int n = 0; n < NT; ++n) {
+        gscore[n] = t1[n] + t2[n];
+        kept[n] = false;
       }
+      for (int r = 0; r < topk_group; ++r) {
+        float bv[NT];
+        int bg[NT];
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          bv[n] = kept[n] ? NEG_INF : gscore[n];
+          bg[n] = g;
+        }
+        MOE_FOR_LEVELS(lgl, LG, {
+          for (int n = 0; n < NT; ++n) {
+            const float ov = partner_f<L_>(bv[n]);
+            const int og = partner_i<L_>(bg[n]);
+            const bool take = (ov > bv[n]) | ((ov == bv[n]) & (og < bg[n]));
+            bv[n] = take ? ov : bv[n];
+            bg[n] = take ? og : bg[n];
+          }
+        })
+#pragma unroll
+        for (int n = 0; n < NT; ++n) kept[n] = kept[n] | (bg[n] == g);
+      }
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int j = 0; j < V; ++j) sel[n][j] = kept[n] ? sel[n][j] : NEG_INF;
     }
   }
 
   // ---- k rounds of group argmax (ties -> lower index, K:1886).  Only the
   // ranked value and its index travel; the sigmoid weight of a winner is
   // recomputed from its logit afterwards (same operations, same bits).
-  int my_id = 0;
-  float my_sel = 0.0f, m0 = 0.0f;
-  float acc = 0.0f;  // sequential slot-order sum the weights divide by
+  int my_id[NT];
+  float my_sel[NT], m0[NT], acc[NT];  // acc: sequential slot-order sum the weights divide by
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    my_id[n] = 0;
+    my_sel[n] = 0.0f;
+    m0[n] = 0.0f;
+    acc[n] = 0.0f;
+  }
 #pragma unroll
   for (int r = 0; r < (KK > 0 ? KK : 8); ++r) {
     if (KK == 0 && r >= k) break;
-    float bv;
-    int bi;
-    local_argmax<V>(sel, e0, bv, bi);
-    MOE_FOR_LEVELS(0, LG, {
-      const float ov = partner_f<L_>(bv);
-      const int oi = partner_i<L_>(bi);
-      // non-short-circuit: a select, not a branch
-      const bool take = (ov > bv) | ((ov == bv) & (oi < bi));
-      bv = take ? ov : bv;
-      bi = take ? oi : bi;
-    })
-    if (gl == r) { my_id = bi; my_sel = bv; }
+    float bv[NT];
+    int bi[NT];
 #pragma unroll
-    for (int j = 0; j < V; ++j)
-      if (e0 + j == bi) sel[j] = NEG_INF;
-    if constexpr (SC == kScoreSoftmax) {
-      if (r == 0) m0 = bv;
-      const float e = det_exp(bv - m0);
-      acc = (r == 0) ? e : acc + e;
-    } else if constexpr (SC == kScoreSoftmaxBias) {
-      acc = (r == 0) ? bv : acc + bv;
+    for (int n = 0; n < NT; ++n) local_argmax<V>(sel[n], e0, bv[n], bi[n]);
+    MOE_FOR_LEVELS(0, LG, {
+      for (int n = 0; n < NT; ++n) {
+        const float ov = partner_f<L_>(bv[n]);
+        const int oi = partner_i<L_>(bi[n]);
+        // non-short-circuit: a select, not a branch
+        const bool take = (ov > bv[n]) | ((ov == bv[n]) & (oi < bi[n]));
+        bv[n] = take ? ov : bv[n];
+        bi[n] = take ? oi : bi[n];
+      }
+    })
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      my_id[n] = gl == r ? bi[n] : my_id[n];
+      my_sel[n] = gl == r ? bv[n] : my_sel[n];
+#pragma unroll
+      for (int j = 0; j < V; ++j) sel[n][j] = e0 + j == bi[n] ? NEG_INF : sel[n][j];
+      if constexpr (SC == kScoreSoftmax) {
+        if (r == 0) m0[n] = bv[n];
+        const float e = det_exp(bv[n] - m0[n]);
+        acc[n] = (r == 0) ? e : acc[n] + e;
+      } else if constexpr (SC == kScoreSoftmaxBias) {
+        acc[n] = (r == 0) ? bv[n] : acc[n] + bv[n];
+      }
     }
   }
   if constexpr (SC == kScoreSigmoidGroup) {
     // a slot's weight is the sigmoid of its expert's logit; the divisor is
     // the sequential slot-order sum of those, read lane by lane from the
     // token's first k lanes
-    float my_aux = 0.0f;
-    if (valid && gl < k) {
-      const float* src = row + my_id;
-      float lv = src[0];
-      for (int p = 1; p < nparts; ++p) lv = lv + src[p * E];
-      my_aux = det_sigmoid(lv);
+    float my_aux[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      my_aux[n] = 0.0f;
+      if (valid[n] && gl < k) {
+        const float* src = row[n] + my_id[n];
+        float lv = src[0];
+        for (int p = 1; p < nparts; ++p) lv = lv + src[p * E];
+        my_aux[n] = det_sigmoid(lv);
+      }
     }
     const int base = (threadIdx.x & 63) - gl;
     for (int r = 0; r < k; ++r) {
-      const float a = __shfl(my_aux, base + r, 64);
-      acc = (r == 0) ? a : acc + a;
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        const float a = __shfl(my_aux[n], base + r, 64);
+        acc[n] = (r == 0) ? a : acc[n] + a;
+      }
     }
-    my_sel = my_aux;  // the weight numerator below
+#pragma unroll
+    for (int n = 0; n < NT; ++n) my_sel[n] = my_aux[n];  // the weight numerator below
   }
 
   // lane gl < k holds slot gl (G >= 8 >= k)
-  {
-    id_out = my_id;
-    w_out = 0.0f;
-    if (valid && gl < k) {
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    id_out[n] = my_id[n];
+    w_out[n] = 0.0f;
+    if (valid[n] && gl < k) {
       float wv;
       if constexpr (SC == kScoreSoftmax) {
-        const float e = det_exp(my_sel - m0);
-        wv = __fdiv_rn(e, renorm ? acc : fullsum) * route_scale;
+        const float e = det_exp(my_sel[n] - m0[n]);
+        wv = __fdiv_rn(e, renorm ? acc[n] : fullsum[n]) * route_scale;
       } else if constexpr (SC == kScoreSigmoidGroup) {
-        wv = (renorm ? __fdiv_rn(my_sel, acc + 1e-20f) : my_sel) * route_scale;
+        wv = (renorm ? __fdiv_rn(my_sel[n], acc[n] + 1e-20f) : my_sel[n]) * route_scale;
       } else {
-        wv = __fdiv_rn(my_sel, fmaxf(acc, norm_min));  // K:1909
+        wv = __fdiv_rn(my_sel[n], fmaxf(acc[n], norm_min));  // K:1909
       }
-      w_out = wv;
+      w_out[n] = wv;
     }
   }
+}
+
+// One token (score_tokens with NT = 1).
+template <int E, int V, int KK, int SC>
+__device__ __forceinline__ void score_token(const float (&l)[V], const float (&b)[V],
+                                            const float* row, int nparts, bool valid, int gl,
+                                            int k_rt, int renorm, int n_group, int topk_group,
+                                            float route_scale, float norm_min, int& id_out,
+                                            float& w_out) {
+  const float(&l1)[1][V] = *reinterpret_cast<const float(*)[1][V]>(&l);
+  const float* const rows[1] = {row};
+  const bool v1[1] = {valid};
+  int id1[1];
+  float w1[1];
+  score_tokens<E, V, KK, SC, 1>(l1, b, rows, nparts, v1, gl, k_rt, renorm, n_group, topk_group,
+                                route_scale, norm_min, id1, w1);
+  id_out = id1[0];
+  w_out = w1[0];
 }
 
 }  // namespace moe

@@ -258,6 +258,26 @@ int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t*
                           const int8_t* ident_a, const float* ident_scales, int ident_m, void* h,
                           void* ws, size_t ws_bytes, void* stream);
 
+/* Measurement aid, no counterpart in the reference: streaming kernels that move
+ * the byte mixes of the HBM-bound stages with sequential addresses (16 bytes per
+ * lane, the cache policies of the stage each models), to measure what this GPU
+ * sustains for each mix beside the real kernels (bench.py --ceiling).
+ *   MOE_PROBE_READ        read `ways` streams src[j*nvec + i] (dst: a 16-byte sink)
+ *   MOE_PROBE_WRITE       write `ways` streams dst[j*nvec + i]
+ *   MOE_PROBE_GATHER_MIX  read nvec vectors of src, write each to `ways`
+ *                         sequential streams dst[j*nvec + i] (dst: ways*nvec)
+ *   MOE_PROBE_COMBINE_MIX read `ways` streams src[j*nvec + i] (src: ways*nvec),
+ *                         write their bf16 sum to dst[i]
+ *   MOE_PROBE_COPY        dst[i] = src[i]
+ * ways in [1, 8]; pointers 16-byte aligned; vectors are 16 bytes. */
+#define MOE_PROBE_READ 0
+#define MOE_PROBE_WRITE 1
+#define MOE_PROBE_GATHER_MIX 2
+#define MOE_PROBE_COMBINE_MIX 3
+#define MOE_PROBE_COPY 4
+int moe_stream_probe(int pattern, const void* src, void* dst, long long nvec, int ways,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -342,3 +342,14 @@ def test_permute_noalloc_validation():
     assert L.moe_permute_workspace_bytes(T_max + 1, 256, 8) > cap
     assert T_max == 131040
     err(perm(T=T_max + 1, H=7168, E=256, k=8), -3, "scratch")
+
+
+def test_stream_probe_validation():
+    L = M.lib()
+    err(L.moe_stream_probe(9, FAKE, FAKE, 16, 1, None), -2, "pattern")
+    err(L.moe_stream_probe(2, FAKE, FAKE, 16, 9, None), -2, "ways")
+    err(L.moe_stream_probe(0, None, FAKE, 16, 1, None), -1)
+    err(L.moe_stream_probe(1, None, None, 16, 1, None), -1)
+    err(L.moe_stream_probe(4, ctypes.c_void_p(0x10008), FAKE, 16, 1, None), -6)
+    err(L.moe_stream_probe(0, FAKE, FAKE, -1, 1, None), -2)
+    assert L.moe_stream_probe(1, None, FAKE, 0, 1, None) == 0
