@@ -85,7 +85,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
   // every wave keeps at most 63 vector loads in flight (the vmcnt limit: the
   // counter does not account for more)
   static_assert(D * (NX + NWF) <= 63, "too many loads in flight per wave");
-  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  __shared__ __attribute__((aligned(1024))) char lds[route_fused_lds(D)];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -320,16 +320,8 @@ static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias
                             int k, int renorm, int n_group, int topk_group, float route_scale,
                             float norm_min, float* logits, int32_t* ids, float* wout,
                             int32_t* counts, hipStream_t s) {
-  constexpr int lds = route_fused_lds(kRfDepth);
   auto kern = route_fused_kernel<kRfWaves, kRfKSplit, kRfDepth, kRfSteps, V, KK, SC, kRfScoreTokens>;
-  static bool attr = false;  // the attribute is per kernel; setting it twice is harmless
-  if (!attr) {
-    const hipError_t e =
-        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
-  hipLaunchKernelGGL(kern, dim3((unsigned)((T + rf::BM - 1) / rf::BM)), dim3(64 * kRfWaves), lds,
+  hipLaunchKernelGGL(kern, dim3((unsigned)((T + rf::BM - 1) / rf::BM)), dim3(64 * kRfWaves), 0,
                      s, x, wf, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min,
                      logits, ids, wout, counts);
   return hipGetLastError();
