@@ -60,13 +60,13 @@ constexpr int route_fused_lds(int D) {
   return (D + 1) * rf::STAGE_B > rf::TILE_B ? (D + 1) * rf::STAGE_B : rf::TILE_B;
 }
 
-// NWV waves (64 * NWV threads, NWV / 4 per SIMD).  KS = 1: wave w owns experts
-// [w*WE, (w+1)*WE) of all 128 rows, both 32-wide K halves of every step.
-// KS = 2: the two waves of a SIMD own the same 64 experts and split every step
-// into its two K halves (wave w does half w / 4); their partial tiles are
-// added in LDS at the end.  Either way a wave's weight slice is its own and
-// goes straight to registers, and x is shared through the LDS ring.
-template <int NWV, int KS, int D, int KTC, int V, int KK, int SC, int NTOK>
+// NWV waves (64 * NWV threads, NWV / 4 per SIMD): wave w owns experts
+// [w*WE, (w+1)*WE) of all 128 rows, so its weight slice is its own and goes
+// straight to registers; x is shared through the LDS ring.  D: K steps of
+// loads in flight.  KTC: the K steps, fully unrolled.  V, KK, SC: the scoring
+// lane width, k (0: runtime) and rule.  NTOK: tokens one 16-lane group scores
+// per pass.
+template <int NWV, int D, int KTC, int V, int KK, int SC, int NTOK>
 __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     const __bf16* __restrict__ x, const __bf16* __restrict__ wf, const float* __restrict__ bias,
     int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
@@ -74,14 +74,11 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     int* __restrict__ counts) {
   using namespace rf;
   constexpr int NT = 64 * NWV;             // threads
-  constexpr int NG = NWV / KS;             // expert groups (waves per K half)
-  constexpr int WE = E / NG;               // experts per wave
+  constexpr int WE = E / NWV;              // experts per wave
   constexpr int NJ = WE / 16;              // 16-expert fragment columns per wave
-  constexpr int KH = 2 / KS;               // 32-wide K halves per wave per step
   constexpr int NX = (BM / 8) / NWV;       // x DMA instructions per wave per stage
-  constexpr int NWF = KH * NJ;             // weight fragments per wave per step
+  constexpr int NWF = 2 * NJ;              // weight fragments per wave per step (two K halves)
   constexpr int NS = D + 1;                // x ring stages
-  static_assert(KS == 1 || NWV == 8, "the K split pairs the two waves of a SIMD");
   // every wave keeps at most 63 vector loads in flight (the vmcnt limit: the
   // counter does not account for more)
   static_assert(D * (NX + NWF) <= 63, "too many loads in flight per wave");
@@ -89,8 +86,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wg = wave % NG;                // expert group
-  const int kw = wave / NG;                // K half (KS = 2)
+  const int wg = wave;                     // expert group
   const long long m0 = (long long)blockIdx.x * BM;
   const int KT = KTC > 0 ? KTC : H / BK;
   const int fr = lane & 15, fc = lane >> 4;
@@ -118,13 +114,11 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
   bf16x8 wr[D][NWF];
   auto issue_w = [&](int kt, bf16x8 (&dst)[NWF]) {
 #pragma unroll
-    for (int h = 0; h < KH; ++h) {
-      const int kk = KS == 2 ? kw : h;
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
-        dst[h * NJ + j] = *reinterpret_cast<const bf16x8*>(
+        dst[kk * NJ + j] = *reinterpret_cast<const bf16x8*>(
             wf + ((long long)((kt * 2 + kk) * 16 + wg * NJ + j) * 64 + lane) * 8);
-    }
   };
   constexpr int VMW = (D - 1) * (NX + NWF);
 
@@ -162,20 +156,20 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
             sb + fr * ROWB + (((kk * 4 + fc) ^ swz(fr)) * 16)));
       };
       bf16x8 a0[8], a1[8];
-      lds_read8(a0, frag_addr(KS == 2 ? kw : 0));
+      lds_read8(a0, frag_addr(0));
       asm volatile("s_waitcnt lgkmcnt(0)"
                    : "+v"(a0[0]), "+v"(a0[1]), "+v"(a0[2]), "+v"(a0[3]), "+v"(a0[4]),
                      "+v"(a0[5]), "+v"(a0[6]), "+v"(a0[7])::"memory");
-      // with both halves: the second half's reads go out before the first
-      // half's MFMAs and land while they run
-      if constexpr (KH == 2) lds_read8(a1, frag_addr(1));
+      // the second half's reads go out before the first half's MFMAs and land
+      // while they run
+      lds_read8(a1, frag_addr(1));
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], wr[u][j], acc[i][j], 0, 0, 0);
-      if constexpr (KH == 2) {
+      {
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt lgkmcnt(0)"
                      : "+v"(a1[0]), "+v"(a1[1]), "+v"(a1[2]), "+v"(a1[3]), "+v"(a1[4]),
@@ -195,30 +189,17 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     }
   }
 
-  // ---- epilogue: the fp32 tile through LDS (KS = 2: the second K half's
-  // partial tile first, then the first half's added onto it)
+  // ---- epilogue: the fp32 tile through LDS
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   float* tile = reinterpret_cast<float*>(lds);
-  auto put = [&](bool add) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int col = wg * WE + j * 16 + fr;
+    for (int j = 0; j < NJ; ++j) {
+      const int col = wg * WE + j * 16 + fr;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float* p = tile + (i * 16 + fc * 4 + r) * TILE_LD + col;
-          *p = add ? acc[i][j][r] + *p : acc[i][j][r];
-        }
-      }
-  };
-  if constexpr (KS == 1) {
-    put(false);
-  } else {
-    if (kw == 1) put(false);
-    __syncthreads();
-    if (kw == 0) put(true);
-  }
+      for (int r = 0; r < 4; ++r) tile[(i * 16 + fc * 4 + r) * TILE_LD + col] = acc[i][j][r];
+    }
   __syncthreads();
 
   // ---- scoring: G = E/V lanes per token
@@ -302,12 +283,12 @@ __global__ void rf_zero_kernel(int* __restrict__ p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// The configuration shipped: 8 waves (two per SIMD) of 32 experts each, one
-// K half each per 32-wide K step pair, weights D = 4 steps ahead, the K loop
+// The configuration shipped: 8 waves (two per SIMD) of 32 experts each,
+// loads D = 4 steps ahead, one token per 16-lane group per scoring pass, the K loop
 // fully unrolled for H = 7168 (112 steps; the DeepSeek-V3 router).  A runtime
 // trip count makes the compiler merge its load bookkeeping at the loop head
 // into a vmcnt(0) that drains every load in flight once per iteration.
-constexpr int kRfWaves = 8, kRfKSplit = 1, kRfDepth = 4, kRfSteps = 112, kRfScoreTokens = 1;
+constexpr int kRfWaves = 8, kRfDepth = 4, kRfSteps = 112, kRfScoreTokens = 1;
 
 bool route_fused_supported(int E, int H, int scoring, int n_group) {
   return E == 256 && H == kRfSteps * rf::BK && topk_lane_width(E, scoring, n_group) == 16;
@@ -320,7 +301,7 @@ static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias
                             int k, int renorm, int n_group, int topk_group, float route_scale,
                             float norm_min, float* logits, int32_t* ids, float* wout,
                             int32_t* counts, hipStream_t s) {
-  auto kern = route_fused_kernel<kRfWaves, kRfKSplit, kRfDepth, kRfSteps, V, KK, SC, kRfScoreTokens>;
+  auto kern = route_fused_kernel<kRfWaves, kRfDepth, kRfSteps, V, KK, SC, kRfScoreTokens>;
   hipLaunchKernelGGL(kern, dim3((unsigned)((T + rf::BM - 1) / rf::BM)), dim3(64 * kRfWaves), 0,
                      s, x, wf, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min,
                      logits, ids, wout, counts);
