@@ -106,10 +106,11 @@ size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype) {
   size_t b = 0;
   if (w_dtype == MOE_DTYPE_FP32) b += round256((size_t)2 * E * H * 2);
   if (parts > 1) b += round256((size_t)T * parts * E * 4);
-  // E = 256, H = 7168, bf16: the fused GEMM + scoring kernel (used unless the
-  // scoring rule needs narrower lanes) keeps a fragment-major weight copy
-  if (w_dtype == MOE_DTYPE_BF16 && E == 256 && H == 7168) {
-    const size_t f = round256(moe::route_fused_workspace_bytes(H));
+  // E = 256, H = 7168 and E = 128, H = 2048 with bf16 weights: the fused GEMM +
+  // scoring kernel (used unless the scoring rule needs narrower lanes) keeps a
+  // fragment-major weight copy
+  if (w_dtype == MOE_DTYPE_BF16 && ((E == 256 && H == 7168) || (E == 128 && H == 2048))) {
+    const size_t f = round256(moe::route_fused_workspace_bytes(E, H));
     if (f > b) b = f;
   }
   return b;
@@ -168,7 +169,7 @@ int moe_route(const void* x, const void* w, int w_dtype, const float* bias, int 
                                      cfg->norm_min, nullptr, topk_ids, topk_w, counts, s),
                     "topk");
   if (w_dtype == MOE_DTYPE_BF16 && moe::route_fused_supported(E, H, cfg->scoring, cfg->n_group))
-    return launched(moe::launch_route_fused((const __bf16*)x, (const __bf16*)w, bias, T, H, k,
+    return launched(moe::launch_route_fused((const __bf16*)x, (const __bf16*)w, bias, T, E, H, k,
                                             cfg->scoring, cfg->renormalize, cfg->n_group,
                                             cfg->topk_group, cfg->route_scale, cfg->norm_min,
                                             logits, topk_ids, topk_w, counts, ws, s),

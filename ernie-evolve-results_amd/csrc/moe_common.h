@@ -47,12 +47,12 @@ hipError_t launch_topk(const float* logits, int nparts, const float* bias, int T
                        int scoring, int renorm, int n_group, int topk_group, float route_scale,
                        float norm_min, float* logits_out, int32_t* ids, float* w,
                        int32_t* counts, hipStream_t s);
-// Router GEMM + scoring in one kernel (E = 256, H = 7168, 16 experts per
-// scoring lane); ws holds route_fused_workspace_bytes(H) bytes.
+// Router GEMM + scoring in one kernel (E = 256, H = 7168 or E = 128, H = 2048,
+// 16 experts per scoring lane); ws holds route_fused_workspace_bytes(E, H) bytes.
 bool route_fused_supported(int E, int H, int scoring, int n_group);
-size_t route_fused_workspace_bytes(int H);
-hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
-                              int k, int scoring, int renorm, int n_group, int topk_group,
+size_t route_fused_workspace_bytes(int E, int H);
+hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bias, int T, int E,
+                              int H, int k, int scoring, int renorm, int n_group, int topk_group,
                               float route_scale, float norm_min, float* logits, int32_t* ids,
                               float* wout, int32_t* counts, void* ws, hipStream_t s);
 hipError_t launch_offsets(const int32_t* counts, int E, int32_t* offsets, hipStream_t s);

@@ -29,44 +29,69 @@
 namespace moe {
 
 namespace rf {
-constexpr int BM = 128, E = 256, BK = 64, ROWB = BK * 2, CH = 8;
-constexpr int STAGE_B = BM * ROWB;        // 16 KB of x per K step
-constexpr int TILE_LD = E + 4;            // fp32 tile row stride (floats) in the epilogue
-constexpr int TILE_B = BM * TILE_LD * 4;  // 133 KB
+constexpr int BK = 64, ROWB = BK * 2, CH = 8;
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & (CH - 1); }
+// BM tokens x E experts per workgroup: the x ring stage (BM rows of one 64-wide
+// K step) and the epilogue's fp32 tile (row stride E + 4 floats)
+constexpr int stage_bytes(int BM) { return BM * ROWB; }
+constexpr int tile_ld(int E) { return E + 4; }
+constexpr int tile_bytes(int BM, int E) { return BM * tile_ld(E) * 4; }
 }  // namespace rf
 
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
 // bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-// Eight 16-byte LDS reads 2 KB apart, issued as one instruction group the
-// compiler does not track; the caller places the lgkmcnt wait (an asm that
-// takes the eight registers as "+v" operands, so nothing reads them before it).
-__device__ __forceinline__ void lds_read8(bf16x8 (&d)[8], unsigned ad) {
-  asm volatile(
-      "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:2048\n\t"
-      "ds_read_b128 %2, %8 offset:4096\n\tds_read_b128 %3, %8 offset:6144\n\t"
-      "ds_read_b128 %4, %8 offset:8192\n\tds_read_b128 %5, %8 offset:10240\n\t"
-      "ds_read_b128 %6, %8 offset:12288\n\tds_read_b128 %7, %8 offset:14336"
-      : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]),
-        "=&v"(d[6]), "=&v"(d[7])
-      : "v"(ad)
-      : "memory");
+// N (8 or 4) 16-byte LDS reads 2 KB apart, issued as one instruction group
+// the compiler does not track (early-clobber outputs: no output may share the
+// address register); the caller places the lgkmcnt wait (an asm that takes
+// the registers as "+v" operands, so nothing reads them before it).
+template <int N>
+__device__ __forceinline__ void lds_readn(bf16x8 (&d)[N], unsigned ad) {
+  static_assert(N == 8 || N == 4, "fragment count");
+  if constexpr (N == 8)
+    asm volatile(
+        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:2048\n\t"
+        "ds_read_b128 %2, %8 offset:4096\n\tds_read_b128 %3, %8 offset:6144\n\t"
+        "ds_read_b128 %4, %8 offset:8192\n\tds_read_b128 %5, %8 offset:10240\n\t"
+        "ds_read_b128 %6, %8 offset:12288\n\tds_read_b128 %7, %8 offset:14336"
+        : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]),
+          "=&v"(d[6]), "=&v"(d[7])
+        : "v"(ad)
+        : "memory");
+  else
+    asm volatile(
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:2048\n\t"
+        "ds_read_b128 %2, %4 offset:4096\n\tds_read_b128 %3, %4 offset:6144"
+        : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3])
+        : "v"(ad)
+        : "memory");
+}
+
+// wait for every outstanding LDS read; the N registers pass through the asm
+template <int N>
+__device__ __forceinline__ void lds_wait(bf16x8 (&d)[N]) {
+  if constexpr (N == 8)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]),
+                   "+v"(d[6]), "+v"(d[7])::"memory");
+  else
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3])::"memory");
 }
 
 // Bytes of LDS the kernel needs: the x ring or the epilogue tile.
-constexpr int route_fused_lds(int D) {
-  return (D + 1) * rf::STAGE_B > rf::TILE_B ? (D + 1) * rf::STAGE_B : rf::TILE_B;
+constexpr int route_fused_lds(int BM, int E, int D) {
+  return (D + 1) * rf::stage_bytes(BM) > rf::tile_bytes(BM, E) ? (D + 1) * rf::stage_bytes(BM)
+                                                                 : rf::tile_bytes(BM, E);
 }
 
-// NWV waves (64 * NWV threads, NWV / 4 per SIMD): wave w owns experts
-// [w*WE, (w+1)*WE) of all 128 rows, so its weight slice is its own and goes
-// straight to registers; x is shared through the LDS ring.  D: K steps of
-// loads in flight.  KTC: the K steps, fully unrolled.  V, KK, SC: the scoring
-// lane width, k (0: runtime) and rule.  NTOK: tokens one 16-lane group scores
-// per pass.
-template <int NWV, int D, int KTC, int V, int KK, int SC, int NTOK>
+// BM tokens (128 or 64) x E experts (256 or 128) per workgroup.  NWV waves
+// (64 * NWV threads, NWV / 4 per SIMD): wave w owns experts [w*WE, (w+1)*WE)
+// of all BM rows, so its weight slice is its own and goes straight to
+// registers; x is shared through the LDS ring.  D: K steps of loads in
+// flight.  KTC: the K steps, fully unrolled.  V, KK, SC: the scoring lane
+// width, k (0: runtime) and rule.  NTOK: tokens one lane group scores per pass.
+template <int BM, int E, int NWV, int D, int KTC, int V, int KK, int SC, int NTOK>
 __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     const __bf16* __restrict__ x, const __bf16* __restrict__ wf, const float* __restrict__ bias,
     int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
@@ -74,6 +99,9 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     int* __restrict__ counts) {
   using namespace rf;
   constexpr int NT = 64 * NWV;             // threads
+  constexpr int FM = BM / 16;              // 16-row fragments per K half
+  constexpr int STAGE_B = stage_bytes(BM);
+  constexpr int TILE_LD = tile_ld(E);
   constexpr int WE = E / NWV;              // experts per wave
   constexpr int NJ = WE / 16;              // 16-expert fragment columns per wave
   constexpr int NX = (BM / 8) / NWV;       // x DMA instructions per wave per stage
@@ -82,7 +110,8 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
   // every wave keeps at most 63 vector loads in flight (the vmcnt limit: the
   // counter does not account for more)
   static_assert(D * (NX + NWF) <= 63, "too many loads in flight per wave");
-  __shared__ __attribute__((aligned(1024))) char lds[route_fused_lds(D)];
+  static_assert(NX >= 1 && NJ >= 1, "tile shape");
+  __shared__ __attribute__((aligned(1024))) char lds[route_fused_lds(BM, E, D)];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -118,13 +147,13 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
         dst[kk * NJ + j] = *reinterpret_cast<const bf16x8*>(
-            wf + ((long long)((kt * 2 + kk) * 16 + wg * NJ + j) * 64 + lane) * 8);
+            wf + ((long long)((kt * 2 + kk) * (E / 16) + wg * NJ + j) * 64 + lane) * 8);
   };
   constexpr int VMW = (D - 1) * (NX + NWF);
 
-  f32x4 acc[8][NJ];
+  f32x4 acc[FM][NJ];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
@@ -149,33 +178,29 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
       __builtin_amdgcn_s_waitcnt(vmcnt_only(VMW));
       __builtin_amdgcn_s_barrier();
       const char* sb = lds + (kt % NS) * STAGE_B;
-      // rows i*16 + fr share the swizzle of fr: a half step's eight fragment
+      // rows i*16 + fr share the swizzle of fr: a half step's FM fragment
       // reads are 2 KB apart
       auto frag_addr = [&](int kk) {
         return (unsigned)(uintptr_t)((__attribute__((address_space(3))) const char*)(
             sb + fr * ROWB + (((kk * 4 + fc) ^ swz(fr)) * 16)));
       };
-      bf16x8 a0[8], a1[8];
-      lds_read8(a0, frag_addr(0));
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(a0[0]), "+v"(a0[1]), "+v"(a0[2]), "+v"(a0[3]), "+v"(a0[4]),
-                     "+v"(a0[5]), "+v"(a0[6]), "+v"(a0[7])::"memory");
+      bf16x8 a0[FM], a1[FM];
+      lds_readn<FM>(a0, frag_addr(0));
+      lds_wait<FM>(a0);
       // the second half's reads go out before the first half's MFMAs and land
       // while they run
-      lds_read8(a1, frag_addr(1));
+      lds_readn<FM>(a1, frag_addr(1));
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], wr[u][j], acc[i][j], 0, 0, 0);
       {
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt lgkmcnt(0)"
-                     : "+v"(a1[0]), "+v"(a1[1]), "+v"(a1[2]), "+v"(a1[3]), "+v"(a1[4]),
-                       "+v"(a1[5]), "+v"(a1[6]), "+v"(a1[7])::"memory");
+        lds_wait<FM>(a1);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
             acc[i][j] =
@@ -193,7 +218,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   float* tile = reinterpret_cast<float*>(lds);
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int col = wg * WE + j * 16 + fr;
@@ -264,15 +289,16 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
   }
 }
 
-// Router weight [256, H] bf16 -> fragment-major copy: fragment f = (kt*2 + kk)*16 + g
-// holds, for lane l, the 8 values w[g*16 + (l & 15)][kt*64 + kk*32 + (l >> 4)*8 ..],
-// so each MFMA B fragment the GEMM loads is 1 KB contiguous.
-__global__ __launch_bounds__(256) void rf_wfrag_kernel(const u32x4* __restrict__ w, int H,
+// Router weight [E, H] bf16 -> fragment-major copy: with NG = E / 16 expert
+// groups, fragment f = (kt*2 + kk)*NG + g holds, for lane l, the 8 values
+// w[g*16 + (l & 15)][kt*64 + kk*32 + (l >> 4)*8 ..], so each MFMA B fragment
+// the GEMM loads is 1 KB contiguous.
+__global__ __launch_bounds__(256) void rf_wfrag_kernel(const u32x4* __restrict__ w, int H, int ng,
                                                         u32x4* __restrict__ wf, int n) {
   const int v = blockIdx.x * 256 + threadIdx.x;
   if (v >= n) return;
   const int l = v & 63, f = v >> 6;
-  const int g = f & 15, kk = (f >> 4) & 1, kt = f >> 5;
+  const int g = f % ng, kk = (f / ng) & 1, kt = f / (2 * ng);
   const int e = g * 16 + (l & 15);
   const int k = kt * 64 + kk * 32 + (l >> 4) * 8;
   wf[v] = w[((long long)e * H + k) / 8];
@@ -283,63 +309,80 @@ __global__ void rf_zero_kernel(int* __restrict__ p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// The configuration shipped: 8 waves (two per SIMD) of 32 experts each,
-// loads D = 4 steps ahead, one token per 16-lane group per scoring pass, the K loop
-// fully unrolled for H = 7168 (112 steps; the DeepSeek-V3 router).  A runtime
-// trip count makes the compiler merge its load bookkeeping at the loop head
-// into a vmcnt(0) that drains every load in flight once per iteration.
-constexpr int kRfWaves = 8, kRfDepth = 4, kRfSteps = 112, kRfScoreTokens = 1;
+// The configurations shipped: 8 waves (two per SIMD; one wave per SIMD issues
+// MFMAs at about a third of the rate), loads D = 4 steps ahead, one token per
+// lane group per scoring pass, the K loop fully unrolled (a runtime trip count
+// makes the compiler merge its load bookkeeping at the loop head into a
+// vmcnt(0) that drains every load in flight once per iteration):
+//   E = 256, H = 7168 (DeepSeek-V3): 128-token tiles, 112 K steps;
+//   E = 128, H = 2048 (Qwen3-MoE):   64-token tiles (256 of them at T = 16384),
+//                                    32 K steps.
+constexpr int kRfWaves = 8, kRfDepth = 4, kRfScoreTokens = 1;
 
 bool route_fused_supported(int E, int H, int scoring, int n_group) {
-  return E == 256 && H == kRfSteps * rf::BK && topk_lane_width(E, scoring, n_group) == 16;
+  const bool shape = (E == 256 && H == 112 * rf::BK) || (E == 128 && H == 32 * rf::BK);
+  return shape && topk_lane_width(E, scoring, n_group) == 16;
 }
 
-size_t route_fused_workspace_bytes(int H) { return (size_t)rf::E * H * 2; }
+size_t route_fused_workspace_bytes(int E, int H) { return (size_t)E * H * 2; }
 
-template <int V, int KK, int SC>
+template <int BM, int E, int KTC, int V, int KK, int SC>
 static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias, int T, int H,
                             int k, int renorm, int n_group, int topk_group, float route_scale,
                             float norm_min, float* logits, int32_t* ids, float* wout,
                             int32_t* counts, hipStream_t s) {
-  auto kern = route_fused_kernel<kRfWaves, kRfDepth, kRfSteps, V, KK, SC, kRfScoreTokens>;
-  hipLaunchKernelGGL(kern, dim3((unsigned)((T + rf::BM - 1) / rf::BM)), dim3(64 * kRfWaves), 0,
-                     s, x, wf, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min,
-                     logits, ids, wout, counts);
+  auto kern = route_fused_kernel<BM, E, kRfWaves, kRfDepth, KTC, V, KK, SC, kRfScoreTokens>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)((T + BM - 1) / BM)), dim3(64 * kRfWaves), 0, s, x, wf,
+                     bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, logits,
+                     ids, wout, counts);
   return hipGetLastError();
 }
 
-// x [T, H] bf16, w [256, H] bf16; ws: route_fused_workspace_bytes(H) bytes
-// (the fragment-major weight copy).  Caller checked route_fused_supported.
-hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
-                              int k, int scoring, int renorm, int n_group, int topk_group,
-                              float route_scale, float norm_min, float* logits, int32_t* ids,
-                              float* wout, int32_t* counts, void* ws, hipStream_t s) {
-  if (counts) {
-    hipLaunchKernelGGL(rf_zero_kernel, dim3(1), dim3(256), 0, s, counts, 256);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-  }
-  if (T == 0) return hipSuccess;
-  __bf16* wf = (__bf16*)ws;
-  {
-    const int n = rf::E * H / 8;
-    hipLaunchKernelGGL(rf_wfrag_kernel, dim3((n + 255) / 256), dim3(256), 0, s, (const u32x4*)w,
-                       H, (u32x4*)wf, n);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-  }
+template <int BM, int E, int KTC>
+static hipError_t launch_rf_cfg(const __bf16* x, const __bf16* wf, const float* bias, int T,
+                                int H, int k, int scoring, int renorm, int n_group, int topk_group,
+                                float route_scale, float norm_min, float* logits, int32_t* ids,
+                                float* wout, int32_t* counts, hipStream_t s) {
 #define MOE_RF_ARGS x, wf, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, \
                     logits, ids, wout, counts, s
-#define MOE_RF_SC(SCV)                                       \
-  {                                                          \
-    if (k == 8) return launch_rf<16, 8, SCV>(MOE_RF_ARGS);   \
-    return launch_rf<16, 0, SCV>(MOE_RF_ARGS);               \
+#define MOE_RF_SC(SCV)                                                  \
+  {                                                                     \
+    if (k == 8) return launch_rf<BM, E, KTC, 16, 8, SCV>(MOE_RF_ARGS);  \
+    return launch_rf<BM, E, KTC, 16, 0, SCV>(MOE_RF_ARGS);              \
   }
   if (scoring == kScoreSoftmax) MOE_RF_SC(kScoreSoftmax)
   if (scoring == kScoreSigmoidGroup) MOE_RF_SC(kScoreSigmoidGroup)
   MOE_RF_SC(kScoreSoftmaxBias)
 #undef MOE_RF_SC
 #undef MOE_RF_ARGS
+}
+
+// x [T, H] bf16, w [E, H] bf16; ws: route_fused_workspace_bytes(E, H) bytes
+// (the fragment-major weight copy).  Caller checked route_fused_supported.
+hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bias, int T, int E,
+                              int H, int k, int scoring, int renorm, int n_group, int topk_group,
+                              float route_scale, float norm_min, float* logits, int32_t* ids,
+                              float* wout, int32_t* counts, void* ws, hipStream_t s) {
+  if (counts) {
+    hipLaunchKernelGGL(rf_zero_kernel, dim3((E + 255) / 256), dim3(256), 0, s, counts, E);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (T == 0) return hipSuccess;
+  __bf16* wf = (__bf16*)ws;
+  {
+    const int n = E * H / 8;
+    hipLaunchKernelGGL(rf_wfrag_kernel, dim3((n + 255) / 256), dim3(256), 0, s, (const u32x4*)w,
+                       H, E / 16, (u32x4*)wf, n);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (E == 256)
+    return launch_rf_cfg<128, 256, 112>(x, wf, bias, T, H, k, scoring, renorm, n_group,
+                                        topk_group, route_scale, norm_min, logits, ids, wout,
+                                        counts, s);
+  return launch_rf_cfg<64, 128, 32>(x, wf, bias, T, H, k, scoring, renorm, n_group, topk_group,
+                                    route_scale, norm_min, logits, ids, wout, counts, s);
 }
 
 }  // namespace moe

@@ -79,9 +79,9 @@ const char* moe_last_error_string(void);
  *     weights (hi and lo halves) or a K split (ksplit > 1, chosen when the
  *     row x expert tiles alone leave the chip's 256 CUs idle, e.g. small T):
  *     [T, parts*E] fp32 partial sums.
- *   - E = 256, H = 7168 with bf16 weights: the router GEMM and the scoring run
- *     as one kernel that reads a fragment-major copy of the weight, E*H*2
- *     bytes (3.5 MiB), rewritten by every call.
+ *   - E = 256, H = 7168 or E = 128, H = 2048 with bf16 weights: the router
+ *     GEMM and the scoring run as one kernel that reads a fragment-major copy
+ *     of the weight, E*H*2 bytes (3.5 MiB / 512 KiB), rewritten by every call.
  * The size does not depend on cfg; it covers whichever path the call takes. */
 size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype);
 

@@ -122,7 +122,7 @@ def _route_ws(T, H, E, fp32):
     parts = (N // E) * _router_ksplit(T, H, N)
     b = r256(2 * E * H * 2) if fp32 else 0
     b += r256(T * parts * E * 4) if parts > 1 else 0
-    if not fp32 and E == 256 and H == 7168:  # fused GEMM + scoring: fragment-major weight copy
+    if not fp32 and (E, H) in ((256, 7168), (128, 2048)):  # fused GEMM + scoring: weight copy
         b = max(b, r256(E * H * 2))
     return b
 

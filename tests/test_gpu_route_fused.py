@@ -1,4 +1,5 @@
-"""The fused router GEMM + scoring kernel (E = 256, H = 7168) against the
+"""The fused router GEMM + scoring kernel (E = 256, H = 7168 with 128-token
+tiles; E = 128, H = 2048 with 64-token tiles) against the
 two-kernel path it replaces (moe_router_gemm, then moe_topk on the logits it
 wrote) and against the oracle on the kernel's own logits.
 
@@ -21,7 +22,7 @@ from oracle import moe_oracle as O
 
 pytestmark = pytest.mark.gpu
 
-H, E = 7168, 256
+SHAPES = [(256, 7168), (128, 2048)]  # (E, H) the fused kernel takes
 
 CFGS = {
     "sigmoid_group": RouteCfg(SCORING_SIGMOID_GROUP, True, 8, 4, 2.5),
@@ -32,7 +33,8 @@ CFGS = {
 
 def two_kernel_route(x, w, bias, k, cfg):
     L = M.lib()
-    T = x.shape[0]
+    T, H = x.shape
+    E = w.shape[0]
     logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
     rc = L.moe_router_gemm(M._ptr(x), M._ptr(w), T, H, E, M._ptr(logits), M._stream(x))
     assert rc == 0, L.moe_last_error_string()
@@ -42,8 +44,11 @@ def two_kernel_route(x, w, bias, k, cfg):
 
 @pytest.mark.parametrize("T", [1, 77, 128, 129, 1000, 4133])
 @pytest.mark.parametrize("rule", ["sigmoid_group", "softmax", "softmax_bias"])
-def test_fused_route_matches_two_kernel_path(cuda, T, rule):
+@pytest.mark.parametrize("E,H", SHAPES)
+def test_fused_route_matches_two_kernel_path(cuda, T, rule, E, H):
     cfg = CFGS[rule]
+    if rule == "sigmoid_group" and E == 128:
+        cfg = RouteCfg(SCORING_SIGMOID_GROUP, True, 4, 2, 2.5)  # 4 groups of 32
     k = 8 if T % 2 else 5
     g = torch.Generator().manual_seed(T * 7 + len(rule))
     x = torch.randn(T, H, generator=g).bfloat16().to(cuda)
@@ -54,7 +59,7 @@ def test_fused_route_matches_two_kernel_path(cuda, T, rule):
     lf, idf, wf, cf = M.route(x, w, bias, k, cfg)
     lo, ido, wo, co = two_kernel_route(x, w, bias, k, cfg)
     torch.cuda.synchronize()
-    print("fused T=%d rule=%s k=%d" % (T, rule, k), flush=True)
+    print("fused E=%d H=%d T=%d rule=%s k=%d" % (E, H, T, rule, k), flush=True)
     assert torch.equal(lf, lo), "logits differ from the standalone GEMM"
     assert torch.equal(idf, ido)
     assert torch.equal(wf, wo)
@@ -70,11 +75,12 @@ def test_fused_route_matches_two_kernel_path(cuda, T, rule):
     assert np.all(np.abs(got - ow) <= 1e-5 * np.abs(ow) + 1e-30)
 
 
-def test_fused_route_workspace_and_repeat(cuda):
+@pytest.mark.parametrize("E,H", SHAPES)
+def test_fused_route_workspace_and_repeat(cuda, E, H):
     """Two calls in a row with the same workspace (rewritten by every call)
     give the same bits; the workspace is checked on the host."""
     T, k = 300, 8
-    cfg = CFGS["sigmoid_group"]
+    cfg = CFGS["sigmoid_group"] if E == 256 else CFGS["softmax"]
     g = torch.Generator().manual_seed(11)
     x = torch.randn(T, H, generator=g).bfloat16().to(cuda)
     w = (torch.randn(E, H, generator=g) * 0.02).bfloat16().to(cuda)
