@@ -39,9 +39,13 @@ __global__ __launch_bounds__(256) void gather_kernel(const u32x4* __restrict__ x
   }
 }
 
+// One pass: a 256-thread block per 256 work items (the kernels still loop, so
+// any grid is correct).  A grid capped at 65536 blocks, each thread looping
+// ~1.75 times, measured 20 us slower for the C4 gather (801 vs 821 us in the
+// step).
 static int grid_for(long long work) {
   long long g = (work + 255) / 256;
-  if (g > 65536) g = 65536;
+  if (g > (1ll << 24)) g = 1ll << 24;
   return (int)(g < 1 ? 1 : g);
 }
 

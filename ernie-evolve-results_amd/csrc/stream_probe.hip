@@ -10,7 +10,7 @@
 
 namespace moe {
 
-constexpr int kProbeGrid = 65536;
+constexpr int kProbeGrid = 1 << 24;
 
 // W = the number of streams (template: each (pattern, W) pair is its own
 // kernel symbol, so a kernel trace tells the probes apart); W = 0: runtime.
