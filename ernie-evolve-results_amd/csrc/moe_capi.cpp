@@ -547,12 +547,14 @@ int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float sca
 
 int moe_stream_probe(int pattern, const void* src, void* dst, long long nvec, int ways,
                      void* stream) {
-  if (pattern < MOE_PROBE_READ || pattern > MOE_PROBE_COPY)
+  const int base = pattern & ~MOE_PROBE_GRID_STRIDE;
+  if (base < MOE_PROBE_READ || base > MOE_PROBE_COPY)
     return fail(MOE_ERR_INVALID_ARG, "unknown probe pattern %d", pattern);
   if (nvec < 0) return fail(MOE_ERR_INVALID_ARG, "nvec=%lld < 0", nvec);
-  if (pattern != MOE_PROBE_COPY && (ways < 1 || ways > 8))
+  if (base != MOE_PROBE_COPY && (ways < 1 || ways > 8))
     return fail(MOE_ERR_INVALID_ARG, "ways=%d not in [1, 8]", ways);
-  if (!dst || (pattern != MOE_PROBE_WRITE && !src))
+  if (nvec > (1LL << 39)) return fail(MOE_ERR_INVALID_ARG, "nvec=%lld too large", nvec);
+  if (!dst || (base != MOE_PROBE_WRITE && !src))
     return fail(MOE_ERR_NULL_POINTER, "src and dst are required");
   if (!aligned16(dst) || (src && !aligned16(src)))
     return fail(MOE_ERR_ALIGNMENT, "src and dst must be 16-byte aligned");

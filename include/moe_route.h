@@ -269,12 +269,16 @@ int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t*
  *   MOE_PROBE_COMBINE_MIX read `ways` streams src[j*nvec + i] (src: ways*nvec),
  *                         write their bf16 sum to dst[i]
  *   MOE_PROBE_COPY        dst[i] = src[i]
- * ways in [1, 8]; pointers 16-byte aligned; vectors are 16 bytes. */
+ * ways in [1, 8]; pointers 16-byte aligned; vectors are 16 bytes.  The default
+ * launch is one pass (a 256-thread block per 256 vectors); OR-ing
+ * MOE_PROBE_GRID_STRIDE into `pattern` runs the same mix as a grid-stride loop
+ * over at most 65536 blocks (neither shape is fastest for every mix). */
 #define MOE_PROBE_READ 0
 #define MOE_PROBE_WRITE 1
 #define MOE_PROBE_GATHER_MIX 2
 #define MOE_PROBE_COMBINE_MIX 3
 #define MOE_PROBE_COPY 4
+#define MOE_PROBE_GRID_STRIDE 0x100
 int moe_stream_probe(int pattern, const void* src, void* dst, long long nvec, int ways,
                      void* stream);
 

@@ -352,4 +352,8 @@ def test_stream_probe_validation():
     err(L.moe_stream_probe(1, None, None, 16, 1, None), -1)
     err(L.moe_stream_probe(4, ctypes.c_void_p(0x10008), FAKE, 16, 1, None), -6)
     err(L.moe_stream_probe(0, FAKE, FAKE, -1, 1, None), -2)
+    err(L.moe_stream_probe(0x105, FAKE, FAKE, 16, 1, None), -2, "pattern")
+    err(L.moe_stream_probe(0x200, FAKE, FAKE, 16, 1, None), -2, "pattern")
+    err(L.moe_stream_probe(0x100, FAKE, FAKE, 1 << 40, 1, None), -2, "too large")
+    assert L.moe_stream_probe(0x101, None, FAKE, 0, 1, None) == 0
     assert L.moe_stream_probe(1, None, FAKE, 0, 1, None) == 0
