@@ -244,8 +244,21 @@ hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_
   const size_t shm_hist = sizeof(unsigned long long) * E * kMaskWords;
   hipLaunchKernelGGL(pair_hist_kernel, dim3(nblk), dim3(kPairsPerBlock), shm_hist, s, ids,
                      npairs, E, nblk, blockcnt);
-  hipError_t err = hipGetLastError();
+  const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
+  return launch_dispatch_from_hist(ids, T, E, k, blockcnt, totals, row_token, pair_row, offsets,
+                                   counts, s);
+}
+
+// The scan and index launches over raw block histograms already in blockcnt
+// (pair_hist_kernel's, or the fused route kernel's epilogue).  T * k > 0.
+hipError_t launch_dispatch_from_hist(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
+                                     int32_t* totals, int32_t* row_token, int32_t* pair_row,
+                                     int32_t* offsets, int32_t* counts, hipStream_t s) {
+  const long long npairs = (long long)T * k;
+  const int nblk = dispatch_blocks(npairs);
+  const size_t shm_hist = sizeof(unsigned long long) * E * kMaskWords;
+  hipError_t err;
   if ((long long)E * nblk <= kSumMax) {
     // few block histograms: every index block sums them itself, no scan launch
     const size_t shm_sum = shm_hist + sizeof(int) * (3 * E + 1);

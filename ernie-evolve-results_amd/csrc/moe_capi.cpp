@@ -116,6 +116,82 @@ size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype) {
   return b;
 }
 
+}  // extern "C"
+
+// Argument checks of moe_route (workspace included).
+static int check_route(const void* x, const void* w, int w_dtype, int T, int H, int E, int k,
+                       const moe_route_cfg* cfg, float* logits, int32_t* topk_ids, float* topk_w,
+                       void* ws, size_t ws_bytes) {
+  int rc = check_topk_shape(T, E, k);
+  if (rc) return rc;
+  if ((rc = check_cfg(cfg, E, k))) return rc;
+  if (w_dtype != MOE_DTYPE_BF16 && w_dtype != MOE_DTYPE_FP32)
+    return fail(MOE_ERR_UNSUPPORTED, "w_dtype=%d (BF16 or FP32 only)", w_dtype);
+  if (!x || !w || !logits || !topk_ids || !topk_w)
+    return fail(MOE_ERR_NULL_POINTER, "x, w, logits, topk_ids and topk_w are required");
+  if (H <= 0 || H % 64 != 0) return fail(MOE_ERR_UNSUPPORTED, "H=%d is not a positive multiple of 64", H);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(logits))
+    return fail(MOE_ERR_ALIGNMENT, "x, w and logits must be 16-byte aligned");
+  const size_t need = moe_route_workspace_bytes(T, H, E, w_dtype);
+  if (need > 0 && (!ws || ws_bytes < need))
+    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
+  if (need > 0 && !aligned16(ws)) return fail(MOE_ERR_ALIGNMENT, "workspace not 16-byte aligned");
+  return MOE_OK;
+}
+
+// Whether route_launch takes the fused kernel (and so can write the permute's
+// block histograms as well).
+static bool route_is_fused(int T, int H, int E, int w_dtype, const moe_route_cfg* cfg) {
+  return T > 0 && w_dtype == MOE_DTYPE_BF16 &&
+         moe::route_fused_supported(E, H, cfg->scoring, cfg->n_group);
+}
+
+// The route's launches over validated arguments.  blockcnt (fused path only,
+// else NULL): also write the permute's raw block histograms.
+static int route_launch(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
+                        int E, int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids,
+                        float* topk_w, int32_t* counts, int32_t* blockcnt, void* ws,
+                        hipStream_t s) {
+  if (T == 0)
+    return launched(moe::launch_topk(nullptr, 1, bias, 0, E, k, cfg->scoring, cfg->renormalize,
+                                     cfg->n_group, cfg->topk_group, cfg->route_scale,
+                                     cfg->norm_min, nullptr, topk_ids, topk_w, counts, s),
+                    "topk");
+  if (route_is_fused(T, H, E, w_dtype, cfg))
+    return launched(moe::launch_route_fused((const __bf16*)x, (const __bf16*)w, bias, T, E, H, k,
+                                            cfg->scoring, cfg->renormalize, cfg->n_group,
+                                            cfg->topk_group, cfg->route_scale, cfg->norm_min,
+                                            logits, topk_ids, topk_w, counts, blockcnt, ws, s),
+                    "route_fused");
+  const int N = w_dtype == MOE_DTYPE_FP32 ? 2 * E : E;
+  const int ksplit = moe::router_gemm_ksplit(T, H, N);
+  const int parts = (N / E) * ksplit;
+  const __bf16* wb = (const __bf16*)w;
+  char* wsp = (char*)ws;
+  int rc;
+  if (w_dtype == MOE_DTYPE_FP32) {
+    // fp32 weights: hi/lo bf16 split (K:1786-1824), one GEMM against [2E,H]
+    __bf16* wpk = (__bf16*)wsp;
+    wsp += round256((size_t)2 * E * H * 2);
+    rc = launched(moe::launch_wsplit((const float*)w, wpk, E, H, s), "wsplit");
+    if (rc) return rc;
+    wb = wpk;
+  }
+  // parts == 1: the GEMM writes the logits; else it writes [T, parts*E]
+  // partial sums and the scoring kernel adds them and writes the logits.
+  float* gout = parts > 1 ? (float*)wsp : logits;
+  rc = launched(moe::launch_router_gemm((const __bf16*)x, wb, T, H, N, ksplit, gout, s),
+                "router_gemm");
+  if (rc) return rc;
+  return launched(moe::launch_topk(gout, parts, bias, T, E, k, cfg->scoring, cfg->renormalize,
+                                   cfg->n_group, cfg->topk_group, cfg->route_scale,
+                                   cfg->norm_min, parts > 1 ? logits : nullptr, topk_ids, topk_w,
+                                   counts, s),
+                  "topk");
+}
+
+extern "C" {
+
 int moe_router_gemm(const void* x, const void* w, int T, int H, int E, float* logits,
                     void* stream) {
   if (!x || !w || !logits) return fail(MOE_ERR_NULL_POINTER, "x, w and logits are required");
@@ -148,56 +224,11 @@ int moe_topk(const float* logits, const float* bias, int T, int E, int k,
 int moe_route(const void* x, const void* w, int w_dtype, const float* bias, int T, int H, int E,
               int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids, float* topk_w,
               int32_t* counts, void* ws, size_t ws_bytes, void* stream) {
-  int rc = check_topk_shape(T, E, k);
+  const int rc = check_route(x, w, w_dtype, T, H, E, k, cfg, logits, topk_ids, topk_w, ws,
+                             ws_bytes);
   if (rc) return rc;
-  if ((rc = check_cfg(cfg, E, k))) return rc;
-  if (w_dtype != MOE_DTYPE_BF16 && w_dtype != MOE_DTYPE_FP32)
-    return fail(MOE_ERR_UNSUPPORTED, "w_dtype=%d (BF16 or FP32 only)", w_dtype);
-  if (!x || !w || !logits || !topk_ids || !topk_w)
-    return fail(MOE_ERR_NULL_POINTER, "x, w, logits, topk_ids and topk_w are required");
-  if (H <= 0 || H % 64 != 0) return fail(MOE_ERR_UNSUPPORTED, "H=%d is not a positive multiple of 64", H);
-  if (!aligned16(x) || !aligned16(w) || !aligned16(logits))
-    return fail(MOE_ERR_ALIGNMENT, "x, w and logits must be 16-byte aligned");
-  const size_t need = moe_route_workspace_bytes(T, H, E, w_dtype);
-  if (need > 0 && (!ws || ws_bytes < need))
-    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
-  if (need > 0 && !aligned16(ws)) return fail(MOE_ERR_ALIGNMENT, "workspace not 16-byte aligned");
-  hipStream_t s = (hipStream_t)stream;
-  if (T == 0)
-    return launched(moe::launch_topk(nullptr, 1, bias, 0, E, k, cfg->scoring, cfg->renormalize,
-                                     cfg->n_group, cfg->topk_group, cfg->route_scale,
-                                     cfg->norm_min, nullptr, topk_ids, topk_w, counts, s),
-                    "topk");
-  if (w_dtype == MOE_DTYPE_BF16 && moe::route_fused_supported(E, H, cfg->scoring, cfg->n_group))
-    return launched(moe::launch_route_fused((const __bf16*)x, (const __bf16*)w, bias, T, E, H, k,
-                                            cfg->scoring, cfg->renormalize, cfg->n_group,
-                                            cfg->topk_group, cfg->route_scale, cfg->norm_min,
-                                            logits, topk_ids, topk_w, counts, ws, s),
-                    "route_fused");
-  const int N = w_dtype == MOE_DTYPE_FP32 ? 2 * E : E;
-  const int ksplit = moe::router_gemm_ksplit(T, H, N);
-  const int parts = (N / E) * ksplit;
-  const __bf16* wb = (const __bf16*)w;
-  char* wsp = (char*)ws;
-  if (w_dtype == MOE_DTYPE_FP32) {
-    // fp32 weights: hi/lo bf16 split (K:1786-1824), one GEMM against [2E,H]
-    __bf16* wpk = (__bf16*)wsp;
-    wsp += round256((size_t)2 * E * H * 2);
-    rc = launched(moe::launch_wsplit((const float*)w, wpk, E, H, s), "wsplit");
-    if (rc) return rc;
-    wb = wpk;
-  }
-  // parts == 1: the GEMM writes the logits; else it writes [T, parts*E]
-  // partial sums and the scoring kernel adds them and writes the logits.
-  float* gout = parts > 1 ? (float*)wsp : logits;
-  rc = launched(moe::launch_router_gemm((const __bf16*)x, wb, T, H, N, ksplit, gout, s),
-                "router_gemm");
-  if (rc) return rc;
-  return launched(moe::launch_topk(gout, parts, bias, T, E, k, cfg->scoring, cfg->renormalize,
-                                   cfg->n_group, cfg->topk_group, cfg->route_scale,
-                                   cfg->norm_min, parts > 1 ? logits : nullptr, topk_ids, topk_w,
-                                   counts, s),
-                  "topk");
+  return route_launch(x, w, w_dtype, bias, T, H, E, k, cfg, logits, topk_ids, topk_w, counts,
+                      nullptr, ws, (hipStream_t)stream);
 }
 
 int moe_offsets(const int32_t* counts, int E, int32_t* offsets, void* stream) {
@@ -253,19 +284,25 @@ static int check_permute(const void* x, int x_dtype, const int32_t* topk_ids, in
 
 // The permute's launches over a validated workspace of
 // moe_permute_workspace_bytes(T, E, k) bytes.
+// hist_ready: the workspace already holds the raw block histograms (written
+// by the fused route kernel), so the histogram launch is skipped; T * k > 0.
 static int permute_launch(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H,
                           int E, int k, int out_dtype, void* xg, float* scales,
                           int32_t* row_token, int32_t* pair_row, int32_t* offsets,
-                          int32_t* counts, void* ws, void* stream) {
+                          int32_t* counts, void* ws, void* stream, bool hist_ready = false) {
   const bool fp8 = out_dtype == MOE_DTYPE_FP8E4M3FN;
   const int elem = x_dtype == MOE_DTYPE_BF16 ? 2 : 4;
   hipStream_t s = (hipStream_t)stream;
   const int nblk = moe::dispatch_blocks((long long)T * k);
   int32_t* blockcnt = (int32_t*)ws;
   int32_t* totals = (int32_t*)((char*)ws + round256((size_t)E * nblk * 4));
-  int rc = launched(moe::launch_dispatch_index(topk_ids, T, E, k, blockcnt, totals, row_token,
-                                               pair_row, offsets, counts, s),
-                    "dispatch_index");
+  int rc = hist_ready
+               ? launched(moe::launch_dispatch_from_hist(topk_ids, T, E, k, blockcnt, totals,
+                                                         row_token, pair_row, offsets, counts, s),
+                          "dispatch_from_hist")
+               : launched(moe::launch_dispatch_index(topk_ids, T, E, k, blockcnt, totals,
+                                                     row_token, pair_row, offsets, counts, s),
+                          "dispatch_index");
   if (rc || !xg || T == 0) return rc;
   if (fp8) return launched(moe::launch_gather_fp8(x, pair_row, T, H, k, xg, scales, s), "gather_fp8");
   return launched(moe::launch_gather(x, elem, pair_row, T, H, k, xg, s), "gather");
@@ -346,6 +383,43 @@ int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int
   if ((rc = noalloc_scratch(stream, &ws))) return rc;
   return permute_launch(x, x_dtype, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
                         pair_row, offsets, counts, ws, stream);
+}
+
+size_t moe_route_permute_workspace_bytes(int T, int H, int E, int k, int w_dtype) {
+  if (T < 0 || H < 0 || E <= 0 || k < 0) return 0;
+  return round256(moe_route_workspace_bytes(T, H, E, w_dtype)) +
+         moe_permute_workspace_bytes(T, E, k);
+}
+
+int moe_route_permute(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
+                      int E, int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids,
+                      float* topk_w, int out_dtype, void* xg, float* scales, int32_t* row_token,
+                      int32_t* pair_row, int32_t* offsets, int32_t* counts, void* ws,
+                      size_t ws_bytes, void* stream) {
+  // every argument of both stages is checked before anything is launched
+  const size_t rneed = round256(moe_route_workspace_bytes(T, H, E, w_dtype));
+  const size_t need = moe_route_permute_workspace_bytes(T, H, E, k, w_dtype);
+  if (!ws || ws_bytes < need)
+    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
+  if (!aligned16(ws)) return fail(MOE_ERR_ALIGNMENT, "workspace not 16-byte aligned");
+  int rc = check_route(x, w, w_dtype, T, H, E, k, cfg, logits, topk_ids, topk_w, ws, rneed);
+  if (rc) return rc;
+  if ((rc = check_permute(x, MOE_DTYPE_BF16, topk_ids, T, H, E, k, out_dtype, xg, scales,
+                          row_token, pair_row)))
+    return rc;
+  hipStream_t s = (hipStream_t)stream;
+  void* pws = (char*)ws + rneed;
+  // Where the route is the fused kernel, it writes the permute's block
+  // histograms in its epilogue and the histogram launch is skipped.  The
+  // route never writes counts here: the index kernel writes them from the
+  // scanned totals.
+  const bool handoff = route_is_fused(T, H, E, w_dtype, cfg) &&
+                       moe::route_fused_block_hist_supported(E, k);
+  rc = route_launch(x, w, w_dtype, bias, T, H, E, k, cfg, logits, topk_ids, topk_w, nullptr,
+                    handoff ? (int32_t*)pws : nullptr, ws, s);
+  if (rc) return rc;
+  return permute_launch(x, MOE_DTYPE_BF16, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
+                        pair_row, offsets, counts, pws, stream, handoff);
 }
 
 int moe_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* topk_w,

@@ -51,14 +51,24 @@ hipError_t launch_topk(const float* logits, int nparts, const float* bias, int T
 // 16 experts per scoring lane); ws holds route_fused_workspace_bytes(E, H) bytes.
 bool route_fused_supported(int E, int H, int scoring, int n_group);
 size_t route_fused_workspace_bytes(int E, int H);
+// Whether the fused kernel can also write the permute's block histograms
+// (blocks of kPairsPerBlock pairs = whole tokens, whole blocks per tile).
+bool route_fused_block_hist_supported(int E, int k);
+// blockcnt (or NULL): raw block histograms [E, dispatch_blocks(T*k)].
 hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bias, int T, int E,
                               int H, int k, int scoring, int renorm, int n_group, int topk_group,
                               float route_scale, float norm_min, float* logits, int32_t* ids,
-                              float* wout, int32_t* counts, void* ws, hipStream_t s);
+                              float* wout, int32_t* counts, int32_t* blockcnt, void* ws,
+                              hipStream_t s);
 hipError_t launch_offsets(const int32_t* counts, int E, int32_t* offsets, hipStream_t s);
 hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
                                  int32_t* totals, int32_t* row_token, int32_t* pair_row,
                                  int32_t* offsets, int32_t* counts, hipStream_t s);
+// launch_dispatch_index without its histogram launch: blockcnt already holds
+// the raw block histograms [E, dispatch_blocks(T*k)].  T * k > 0.
+hipError_t launch_dispatch_from_hist(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
+                                     int32_t* totals, int32_t* row_token, int32_t* pair_row,
+                                     int32_t* offsets, int32_t* counts, hipStream_t s);
 hipError_t launch_gather(const void* x, int elem_bytes, const int32_t* pair_row, int T, int H,
                          int k, void* xg, hipStream_t s);
 hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, int T, int H, int k,

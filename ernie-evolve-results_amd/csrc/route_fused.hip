@@ -22,7 +22,9 @@
 //   epilogue    the 128 x 256 fp32 tile goes through LDS once; 16 lanes per
 //               token score it (the scoring kernel's per-token routine,
 //               bit-identical selection), write router_logits row by row,
-//               the ids and weights, and the block's expert histogram.
+//               the ids and weights, and the block's expert histogram --
+//               optionally one per 256 (token, slot) pairs, the permute's
+//               block histograms, so the permute needs no histogram pass.
 #include "moe_common.h"
 #include "score_token.h"
 
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     const __bf16* __restrict__ x, const __bf16* __restrict__ wf, const float* __restrict__ bias,
     int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
     float norm_min, float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ wout,
-    int* __restrict__ counts) {
+    int* __restrict__ counts, int* __restrict__ blockcnt, int nblk, int pt_log2) {
   using namespace rf;
   constexpr int NT = 64 * NWV;             // threads
   constexpr int FM = BM / 16;              // 16-row fragments per K half
@@ -230,9 +232,14 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
   // ---- scoring: G = E/V lanes per token
   constexpr int G = E / V;
   constexpr int TPP = NT / G;  // tokens per pass
-  __shared__ int hist[E];
-  if (counts) {
-    for (int i = threadIdx.x; i < E; i += NT) hist[i] = 0;
+  // expert histograms of the tile's sub-blocks of 2^pt_log2 tokens (with
+  // blockcnt: the permute's blocks of 256 pairs, 256 / k tokens each; without:
+  // pt_log2 >= log2(BM), one histogram for the whole tile)
+  constexpr int MAXSB = BM / 32;
+  __shared__ int hist[MAXSB * E];
+  const bool hists = counts || blockcnt;
+  if (hists) {
+    for (int i = threadIdx.x; i < MAXSB * E; i += NT) hist[i] = 0;
     __syncthreads();
   }
   const int gl = threadIdx.x % G;
@@ -276,15 +283,28 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
       if (valid[n] && gl < k) {
         ids[t * k + gl] = my_id[n];
         wout[t * k + gl] = wv[n];
-        if (counts) atomicAdd(&hist[my_id[n]], 1);
+        if (hists) atomicAdd(&hist[((tl0 + n * TPP) >> pt_log2) * E + my_id[n]], 1);
       }
     }
   }
-  if (counts) {
+  if (hists) {
     __syncthreads();
-    for (int i = threadIdx.x; i < E; i += NT) {
-      const int c = hist[i];
-      if (c) atomicAdd(counts + i, c);
+    const int nsb = pt_log2 >= 31 ? 1 : (BM >> pt_log2 > 0 ? BM >> pt_log2 : 1);
+    if (counts) {
+      for (int i = threadIdx.x; i < E; i += NT) {
+        int c = 0;
+        for (int b = 0; b < nsb; ++b) c += hist[b * E + i];
+        if (c) atomicAdd(counts + i, c);
+      }
+    }
+    if (blockcnt) {
+      // [E, nblk] layout: the tile's nsb consecutive blocks of one expert are
+      // adjacent; blocks past the last pair are not written
+      const int b0 = (int)(m0 >> pt_log2);
+      for (int i = threadIdx.x; i < nsb * E; i += NT) {
+        const int e = i / nsb, b = i - e * nsb;
+        if (b0 + b < nblk) blockcnt[(long long)e * nblk + b0 + b] = hist[b * E + e];
+      }
     }
   }
 }
@@ -324,17 +344,34 @@ bool route_fused_supported(int E, int H, int scoring, int n_group) {
   return shape && topk_lane_width(E, scoring, n_group) == 16;
 }
 
+// Token tile of the shipped configuration of this shape.
+static int rf_tile_tokens(int E) { return E == 256 ? 128 : 64; }
+
+bool route_fused_block_hist_supported(int E, int k) {
+  // blocks of kPairsPerBlock pairs hold whole tokens, and a tile whole blocks
+  return k >= 1 && k <= 8 && kPairsPerBlock % k == 0 &&
+         rf_tile_tokens(E) % (kPairsPerBlock / k) == 0;
+}
+
 size_t route_fused_workspace_bytes(int E, int H) { return (size_t)E * H * 2; }
 
 template <int BM, int E, int KTC, int V, int KK, int SC>
 static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias, int T, int H,
                             int k, int renorm, int n_group, int topk_group, float route_scale,
                             float norm_min, float* logits, int32_t* ids, float* wout,
-                            int32_t* counts, hipStream_t s) {
+                            int32_t* counts, int32_t* blockcnt, hipStream_t s) {
   auto kern = route_fused_kernel<BM, E, kRfWaves, kRfDepth, KTC, V, KK, SC, kRfScoreTokens>;
+  // blocks of 256 pairs = 2^pt_log2 tokens (k a power of two), else one
+  // histogram per tile
+  int pt_log2 = 31;
+  if (blockcnt) {
+    pt_log2 = 0;
+    while ((k << pt_log2) < kPairsPerBlock) ++pt_log2;
+  }
+  const int nblk = dispatch_blocks((long long)T * k);
   hipLaunchKernelGGL(kern, dim3((unsigned)((T + BM - 1) / BM)), dim3(64 * kRfWaves), 0, s, x, wf,
                      bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, logits,
-                     ids, wout, counts);
+                     ids, wout, counts, blockcnt, nblk, pt_log2);
   return hipGetLastError();
 }
 
@@ -342,9 +379,9 @@ template <int BM, int E, int KTC>
 static hipError_t launch_rf_cfg(const __bf16* x, const __bf16* wf, const float* bias, int T,
                                 int H, int k, int scoring, int renorm, int n_group, int topk_group,
                                 float route_scale, float norm_min, float* logits, int32_t* ids,
-                                float* wout, int32_t* counts, hipStream_t s) {
+                                float* wout, int32_t* counts, int32_t* blockcnt, hipStream_t s) {
 #define MOE_RF_ARGS x, wf, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, \
-                    logits, ids, wout, counts, s
+                    logits, ids, wout, counts, blockcnt, s
 #define MOE_RF_SC(SCV)                                                  \
   {                                                                     \
     if (k == 8) return launch_rf<BM, E, KTC, 16, 8, SCV>(MOE_RF_ARGS);  \
@@ -359,10 +396,13 @@ static hipError_t launch_rf_cfg(const __bf16* x, const __bf16* wf, const float* 
 
 // x [T, H] bf16, w [E, H] bf16; ws: route_fused_workspace_bytes(E, H) bytes
 // (the fragment-major weight copy).  Caller checked route_fused_supported.
+// blockcnt (or NULL): the permute's raw block histograms [E, ceil(T*k/256)],
+// every entry written; needs route_fused_block_hist_supported(E, k).
 hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bias, int T, int E,
                               int H, int k, int scoring, int renorm, int n_group, int topk_group,
                               float route_scale, float norm_min, float* logits, int32_t* ids,
-                              float* wout, int32_t* counts, void* ws, hipStream_t s) {
+                              float* wout, int32_t* counts, int32_t* blockcnt, void* ws,
+                              hipStream_t s) {
   if (counts) {
     hipLaunchKernelGGL(rf_zero_kernel, dim3((E + 255) / 256), dim3(256), 0, s, counts, E);
     const hipError_t err = hipGetLastError();
@@ -380,9 +420,10 @@ hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bia
   if (E == 256)
     return launch_rf_cfg<128, 256, 112>(x, wf, bias, T, H, k, scoring, renorm, n_group,
                                         topk_group, route_scale, norm_min, logits, ids, wout,
-                                        counts, s);
+                                        counts, blockcnt, s);
   return launch_rf_cfg<64, 128, 32>(x, wf, bias, T, H, k, scoring, renorm, n_group, topk_group,
-                                    route_scale, norm_min, logits, ids, wout, counts, s);
+                                    route_scale, norm_min, logits, ids, wout, counts, blockcnt,
+                                    s);
 }
 
 }  // namespace moe

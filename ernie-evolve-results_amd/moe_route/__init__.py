@@ -35,7 +35,8 @@ EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
            "moe_grouped_gemm_fp8", "moe_grouped_swiglu_fp8", "moe_quant_rows_i8",
            "moe_grouped_gemm_i8", "moe_grouped_swiglu_i8", "moe_grouped_gemm_rows",
            "moe_grouped_swiglu_rows", "moe_permute_noalloc_max_scratch_bytes",
-           "moe_permute_noalloc", "moe_stream_probe"]
+           "moe_permute_noalloc", "moe_stream_probe", "moe_route_permute_workspace_bytes",
+           "moe_route_permute"]
 
 
 class MoeError(RuntimeError):
@@ -90,6 +91,11 @@ def lib():
         L.moe_permute_noalloc.restype = _I
         L.moe_permute_noalloc.argtypes = [_P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P,
                                           _P]
+        L.moe_route_permute_workspace_bytes.restype = _Z
+        L.moe_route_permute_workspace_bytes.argtypes = [_I, _I, _I, _I, _I]
+        L.moe_route_permute.restype = _I
+        L.moe_route_permute.argtypes = [_P, _P, _I, _P, _I, _I, _I, _I, ctypes.POINTER(_Cfg), _P,
+                                        _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _Z, _P]
         L.moe_stream_probe.restype = _I
         L.moe_stream_probe.argtypes = [_I, _P, _P, ctypes.c_longlong, _I, _P]
         L.moe_combine.restype = _I
@@ -635,6 +641,11 @@ class MoePlan:
         self.ws_route = torch.empty(max(self.nws_route, 256), dtype=torch.uint8, device=dev)
         self.nws_perm = L.moe_permute_workspace_bytes(T, E, k)
         self.ws_perm = torch.empty(max(self.nws_perm, 256), dtype=torch.uint8, device=dev)
+        # one call for route + permute (bf16 x): the route's and the permute's
+        # workspaces back to back
+        self.nws_rp = L.moe_route_permute_workspace_bytes(T, H, E, k, self.wd)
+        self.ws_rp = (torch.empty(max(self.nws_rp, 256), dtype=torch.uint8, device=dev)
+                      if x_dtype == torch.bfloat16 else None)
 
     def route(self, x, w, bias, counts=False):
         """Router GEMM + scoring + top-k.  The per-expert counts are also
@@ -674,6 +685,25 @@ class MoePlan:
                                  _ptr(self.counts), _ptr(self.ws_perm), self.nws_perm,
                                  _stream(x)))
 
+    def route_permute(self, x, w, bias, index_only=False):
+        """``route`` then ``permute`` in one C-ABI call (moe_route_permute):
+        the same outputs; where the route is the fused kernel its epilogue
+        also writes the permute's block histograms.  bf16 x only."""
+        if self.ws_rp is None:
+            raise RuntimeError("route_permute needs bf16 x")
+        _want(x, "x", _BF16, (self.T, self.H))
+        _want(w, "w", (self.w_dtype,), (self.E, self.H))
+        if bias is not None:
+            _want(bias, "bias", _F32, (self.E,))
+        _devs(x=x, w=w, bias=bias)
+        od = DTYPE_FP8E4M3FN if self.fp8 else self.xd
+        _check(lib().moe_route_permute(
+            _ptr(x), _ptr(w), self.wd, _ptr(bias), self.T, self.H, self.E, self.k,
+            ctypes.byref(self.cfg), _ptr(self.logits), _ptr(self.topk_ids), _ptr(self.topk_w), od,
+            None if index_only else _ptr(self.xg), _ptr(self.scales), _ptr(self.row_token),
+            _ptr(self.pair_row), _ptr(self.offsets), _ptr(self.counts), _ptr(self.ws_rp),
+            self.nws_rp, _stream(x)))
+
     def combine(self, y, shared=None):
         if y is None:  # identity experts: combine the gathered rows
             if self.fp8:
@@ -691,8 +721,12 @@ class MoePlan:
     def step(self, x, w, bias, y):
         """route -> permute -> combine for one batch.  y None: identity experts
         (the C1 configuration), i.e. the gathered rows are combined, which
-        returns x when the weights sum to 1."""
-        self.route(x, w, bias)
-        self.permute(x)
+        returns x when the weights sum to 1.  bf16 x: route and permute are
+        one call (``route_permute``)."""
+        if self.ws_rp is not None:
+            self.route_permute(x, w, bias)
+        else:
+            self.route(x, w, bias)
+            self.permute(x)
         self.combine(y)
         return self.out

@@ -154,6 +154,26 @@ int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int
                         int k, int out_dtype, void* xg, float* scales, int32_t* row_token,
                         int32_t* pair_row, int32_t* offsets, int32_t* counts, void* stream);
 
+/* Stages 1-4 in one call: moe_route, then moe_permute on its ids (bf16 x;
+ * out_dtype BF16 or FP8E4M3FN; xg NULL = index only), with the same outputs
+ * bit for bit as the two calls.  Replaces run()'s sequence K:4323-4431
+ * (wsplit, router GEMM, topk_kernel, offsets_kernel, dispatch and gather).
+ * Where the route is one fused kernel (bf16 weights, E = 256 with H = 7168 or
+ * E = 128 with H = 2048) and k divides 256 with 256 / k tokens fitting its
+ * token tile (k in {2, 4, 8} at E = 256, {4, 8} at E = 128), that kernel's
+ * epilogue writes the permute's per-block expert histograms into the
+ * workspace and the permute's histogram launch is skipped; otherwise the two
+ * stages run as moe_route and moe_permute would.  counts: the permute's.
+ * ws: moe_route_permute_workspace_bytes(T, H, E, k, w_dtype) bytes, 16-byte
+ * aligned (the route's workspace, rounded up to 256 bytes, then the
+ * permute's).  Every argument of both stages is checked before any launch. */
+size_t moe_route_permute_workspace_bytes(int T, int H, int E, int k, int w_dtype);
+int moe_route_permute(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
+                      int E, int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids,
+                      float* topk_w, int out_dtype, void* xg, float* scales, int32_t* row_token,
+                      int32_t* pair_row, int32_t* offsets, int32_t* counts, void* ws,
+                      size_t ws_bytes, void* stream);
+
 /* Stage 5: weighted combine.  Replaces combine_kernel K:2365-2428:
  *   out[t] = cast(shared[t] + sum_j topk_w[t,j] * y[pair_row[t,j]])
  * accumulated in fp32 in slot order.  y [R,H] and out [T,H] of y_dtype (BF16

@@ -60,6 +60,17 @@ int main() {
   // fp32 weights: [2E,H] bf16 hi/lo split + [T,2E] fp32 hi/lo partial logits
   if (moe_route_workspace_bytes(32768, 7168, 256, MOE_DTYPE_FP32) != (size_t)2 * 256 * 7168 * 2 + (size_t)32768 * 512 * 4) ++failures;
   if (moe_permute_workspace_bytes(32768, 256, 8) != (size_t)256 * 1024 * 4 + 1024) ++failures;
+  // route + permute in one call: the workspace and both stages' checks come first
+  {
+    moe_route_cfg rc{MOE_SCORING_SOFTMAX, 1, 1, 1, 1.0f, 0.0f};
+    const size_t rp = moe_route_permute_workspace_bytes(16, 128, 8, 2, MOE_DTYPE_BF16);
+    if (rp != ((moe_route_workspace_bytes(16, 128, 8, MOE_DTYPE_BF16) + 255) / 256) * 256 +
+                  moe_permute_workspace_bytes(16, 8, 2))
+      ++failures;
+    EXPECT(moe_route_permute(fake, fake, 0, nullptr, 16, 128, 8, 2, &rc, fp, ip, fp, 0, fake, nullptr, ip, ip, ip, ip, nullptr, rp, nullptr), MOE_ERR_WORKSPACE);
+    EXPECT(moe_route_permute(fake, fake, 0, nullptr, 16, 128, 8, 2, &rc, fp, ip, fp, 1, fake, nullptr, ip, ip, ip, ip, fake, rp, nullptr), MOE_ERR_UNSUPPORTED);
+    EXPECT(moe_route_permute(fake, fake, 0, nullptr, 16, 128, 8, 2, &rc, fp, ip, fp, 0, fake, nullptr, nullptr, ip, ip, ip, fake, rp, nullptr), MOE_ERR_NULL_POINTER);
+  }
   if (moe_version() != MOE_ROUTE_VERSION) ++failures;
   std::printf("%s (%d failures)\n", failures ? "FAILED" : "OK", failures);
   return failures ? 1 : 0;

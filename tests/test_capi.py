@@ -357,3 +357,33 @@ def test_stream_probe_validation():
     err(L.moe_stream_probe(0x100, FAKE, FAKE, 1 << 40, 1, None), -2, "too large")
     assert L.moe_stream_probe(0x101, None, FAKE, 0, 1, None) == 0
     assert L.moe_stream_probe(1, None, FAKE, 0, 1, None) == 0
+
+
+def test_route_permute_workspace_and_validation():
+    """moe_route_permute: workspace = the route's (rounded up to 256 bytes)
+    then the permute's; every argument of both stages is checked before any
+    launch."""
+    L = M.lib()
+    r256 = lambda n: (n + 255) // 256 * 256
+    for (T, H, E, k) in [(32768, 7168, 256, 8), (16384, 2048, 128, 8), (100, 128, 8, 2),
+                         (0, 7168, 256, 8), (4133, 7168, 256, 5)]:
+        assert L.moe_route_permute_workspace_bytes(T, H, E, k, 0) == \
+            r256(L.moe_route_workspace_bytes(T, H, E, 0)) + L.moe_permute_workspace_bytes(T, E, k)
+    assert L.moe_route_permute_workspace_bytes(-1, 7168, 256, 8, 0) == 0
+    c = cfg()
+    need = L.moe_route_permute_workspace_bytes(16, 128, 8, 2, 0)
+
+    def args(T=16, H=128, E=8, k=2, x=FAKE, od=0, xg=FAKE, rt=FAKE, ws=FAKE, nws=None):
+        n = L.moe_route_permute_workspace_bytes(T, H, E, k, 0) if nws is None else nws
+        return (x, FAKE, 0, None, T, H, E, k, ctypes.byref(c), FAKE, FAKE, FAKE, od, xg, None,
+                rt, FAKE, FAKE, FAKE, ws, n, None)
+
+    err(L.moe_route_permute(*args(ws=None)), -4, "workspace")
+    err(L.moe_route_permute(*args(nws=need - 1)), -4, "workspace")
+    err(L.moe_route_permute(*args(ws=ctypes.c_void_p(0x10008))), -6, "aligned")
+    err(L.moe_route_permute(*args(k=9, E=16)), -2)
+    err(L.moe_route_permute(*args(E=12)), -3, "E=12")
+    err(L.moe_route_permute(*args(x=None)), -1)
+    err(L.moe_route_permute(*args(od=1)), -3, "out_dtype")
+    err(L.moe_route_permute(*args(od=2, H=64)), -3, "H % 128")
+    err(L.moe_route_permute(*args(rt=None)), -1, "row_token")
