@@ -19,12 +19,13 @@
 //               w loads share the in-order vmcnt counter: waiting for a
 //               step's weights retires its x stage too, and a wave never has
 //               more than 63 loads in flight (the counter's limit).
-//   epilogue    the 128 x 256 fp32 tile goes through LDS once; 16 lanes per
-//               token score it (the scoring kernel's per-token routine,
-//               bit-identical selection), write router_logits row by row,
-//               the ids and weights, and the block's expert histogram --
-//               optionally one per 256 (token, slot) pairs, the permute's
-//               block histograms, so the permute needs no histogram pass.
+//   epilogue    the 128 x 256 fp32 tile goes through LDS once; 8 lanes per
+//               token (16 at E = 128) score it with the scoring kernel's
+//               per-token routine (bit-identical selection), write
+//               router_logits row by row, the ids and weights, and the
+//               block's expert histogram -- optionally one per 256 (token,
+//               slot) pairs, the permute's block histograms, so the permute
+//               needs no histogram pass.
 #include "moe_common.h"
 #include "score_token.h"
 
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
 #pragma unroll
   for (int j = 0; j < V; ++j) bl[j] = bias ? bias[e0 + j] : 0.0f;
   const int k = KK > 0 ? KK : k_rt;
-  // each 16-lane group scores NTOK tokens per pass (tl, tl + TPP, ...); two or
+  // each G-lane group scores NTOK tokens per pass (tl, tl + TPP, ...); two or
   // four interleaved tokens measured no faster than one (175-180 us per call)
   static_assert(BM % (TPP * NTOK) == 0, "token passes");
   for (int tl0 = threadIdx.x / G; tl0 < BM; tl0 += TPP * NTOK) {
@@ -339,9 +340,18 @@ __global__ void rf_zero_kernel(int* __restrict__ p, int n) {
 //                                    32 K steps.
 constexpr int kRfWaves = 8, kRfDepth = 4, kRfScoreTokens = 1;
 
+// Experts per scoring lane: 32 at E = 256 (8 lanes per token; a DeepSeek-V3
+// group of 32 is one lane, so its top-2 needs no lane exchange: 4-6 us less
+// per call than 16), 16 at E = 128 (a 64-token tile has no room for fewer
+// lanes per token).  A group-limited rule needs whole groups per lane.
+constexpr int rf_lane_width(int E) { return E == 256 ? 32 : 16; }
+
 bool route_fused_supported(int E, int H, int scoring, int n_group) {
   const bool shape = (E == 256 && H == 112 * rf::BK) || (E == 128 && H == 32 * rf::BK);
-  return shape && topk_lane_width(E, scoring, n_group) == 16;
+  if (!shape) return false;
+  if (scoring == kScoreSigmoidGroup && n_group > 1)
+    return n_group <= E && E % n_group == 0 && (E / n_group) % rf_lane_width(E) == 0;
+  return true;
 }
 
 // Token tile of the shipped configuration of this shape.
@@ -384,8 +394,8 @@ static hipError_t launch_rf_cfg(const __bf16* x, const __bf16* wf, const float* 
                     logits, ids, wout, counts, blockcnt, s
 #define MOE_RF_SC(SCV)                                                  \
   {                                                                     \
-    if (k == 8) return launch_rf<BM, E, KTC, 16, 8, SCV>(MOE_RF_ARGS);  \
-    return launch_rf<BM, E, KTC, 16, 0, SCV>(MOE_RF_ARGS);              \
+    if (k == 8) return launch_rf<BM, E, KTC, rf_lane_width(E), 8, SCV>(MOE_RF_ARGS);  \
+    return launch_rf<BM, E, KTC, rf_lane_width(E), 0, SCV>(MOE_RF_ARGS);              \
   }
   if (scoring == kScoreSoftmax) MOE_RF_SC(kScoreSoftmax)
   if (scoring == kScoreSigmoidGroup) MOE_RF_SC(kScoreSigmoidGroup)
