@@ -8,7 +8,8 @@ fitting its token tile (E = 256: k in {2, 4, 8}; E = 128: k in {4, 8}), the
 fused kernel's epilogue writes the permute's block histograms, so these
 cases check that handoff: token counts that end inside a block of 256 pairs
 and inside a route tile (1, 33, 129, 1000, 4133), k = 5 and k = 1 (no
-handoff), and an unfused shape (E = 64).  Needs an MI355X."""
+handoff), an unfused shape (E = 64) and fp32 weights (the hi/lo split
+route of the reference's run() shape).  Needs an MI355X."""
 import ctypes
 
 import pytest
@@ -43,6 +44,10 @@ def outputs(T, H, E, k, fp8, dev):
     }
 
 
+def wcode(w):
+    return M.DTYPE_FP32 if w.dtype == torch.float32 else BF16
+
+
 def run_pair(x, w, bias, k, cfg, fp8, index_only):
     """moe_route then moe_permute (the reference sequence)."""
     L = M.lib()
@@ -50,10 +55,10 @@ def run_pair(x, w, bias, k, cfg, fp8, index_only):
     E = w.shape[0]
     o = outputs(T, H, E, k, fp8, x.device)
     c = M._ccfg(cfg)
-    nr = L.moe_route_workspace_bytes(T, H, E, BF16)
+    nr = L.moe_route_workspace_bytes(T, H, E, wcode(w))
     wr = torch.empty(max(nr, 256), dtype=torch.uint8, device=x.device)
     P = M._ptr
-    M._check(L.moe_route(P(x), P(w), BF16, P(bias), T, H, E, k, ctypes.byref(c), P(o["logits"]),
+    M._check(L.moe_route(P(x), P(w), wcode(w), P(bias), T, H, E, k, ctypes.byref(c), P(o["logits"]),
                          P(o["ids"]), P(o["w"]), None, P(wr), nr, M._stream(x)))
     npm = L.moe_permute_workspace_bytes(T, E, k)
     wp = torch.empty(max(npm, 256), dtype=torch.uint8, device=x.device)
@@ -70,11 +75,11 @@ def run_one(x, w, bias, k, cfg, fp8, index_only, ws_bytes=None):
     E = w.shape[0]
     o = outputs(T, H, E, k, fp8, x.device)
     c = M._ccfg(cfg)
-    need = L.moe_route_permute_workspace_bytes(T, H, E, k, BF16)
+    need = L.moe_route_permute_workspace_bytes(T, H, E, k, wcode(w))
     # the workspace starts dirty: every call writes all it reads
     ws = torch.full((max(need, 256),), 0x5A, dtype=torch.uint8, device=x.device)
     P = M._ptr
-    rc = L.moe_route_permute(P(x), P(w), BF16, P(bias), T, H, E, k, ctypes.byref(c),
+    rc = L.moe_route_permute(P(x), P(w), wcode(w), P(bias), T, H, E, k, ctypes.byref(c),
                              P(o["logits"]), P(o["ids"]), P(o["w"]), FP8 if fp8 else BF16,
                              None if index_only else P(o["xg"]), P(o["scales"]) if fp8 else None,
                              P(o["row_token"]), P(o["pair_row"]), P(o["offsets"]), P(o["counts"]),
@@ -111,6 +116,7 @@ CASES = [
     (128, 2048, 4, 1000, False, False),    # 64-token blocks = one tile
     (128, 2048, 2, 200, False, False),     # no handoff: 128-token blocks > tile
     (64, 1024, 8, 1000, False, False),     # unfused route
+    (64, 8192, 8, 1571, False, True),      # fp32 weights (hi/lo split): the run() shape
 ]
 
 
@@ -120,7 +126,8 @@ def test_route_permute_matches_two_calls(cuda, E, H, k, T, fp8, index_only):
           flush=True)
     g = torch.Generator().manual_seed(E + k * 7 + T)
     x = torch.randn(T, H, generator=g).bfloat16().to(cuda)
-    w = (torch.randn(E, H, generator=g) * 0.02).bfloat16().to(cuda)
+    w = torch.randn(E, H, generator=g) * 0.02
+    w = (w if H == 8192 else w.bfloat16()).to(cuda)
     bias = (torch.randn(E, generator=g) * 0.1).to(cuda)
     cfg = cfg_for(E)
     ref = run_pair(x, w, bias, k, cfg, fp8, index_only)
