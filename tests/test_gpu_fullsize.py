@@ -78,6 +78,18 @@ def test_full_size_route_dispatch_combine(cuda, name):
     mag = combine_ref(y.abs(), r["pair_row"], r["topk_w"].abs(), T, k)
     tol = ref.abs() * 2.0 ** -7 + mag * 2.0 ** -19 + 1e-30
     assert bool(((r["out"].float() - ref).abs() <= tol).all())
+    # the step as bench.py runs it (route + permute in one call: at C3 / C4
+    # the fused route kernel hands the permute its block histograms) gives
+    # the same bits as the separate calls above
+    del ref, mag
+    plan = M.MoePlan(T, c.H, E, k, c.cfg, cuda)
+    out = plan.step(x, w, bias, y)
+    torch.cuda.synchronize()
+    for key, a in (("logits", plan.logits), ("topk_ids", plan.topk_ids), ("topk_w", plan.topk_w),
+                   ("row_token", plan.row_token), ("pair_row", plan.pair_row),
+                   ("offsets", plan.offsets), ("counts", plan.counts), ("xg", plan.xg),
+                   ("out", out)):
+        assert torch.equal(a, r[key]), key
 
 
 def test_full_size_fp8_dispatch_c5(cuda):
@@ -99,6 +111,14 @@ def test_full_size_fp8_dispatch_c5(cuda):
     deq = p["xg"][rows].view(torch.float8_e4m3fn).float().view(len(rows), -1, 128) * sc
     ref = x[toks].float().view(len(rows), -1, 128)
     assert bool(((deq - ref).abs() <= ref.abs() * 2.0 ** -4 * 1.0001 + sc * 2.0 ** -10).all())
+    # route + fp8 permute in one call (the fused route kernel's block
+    # histograms) gives the same bits as the two calls
+    del deq, ref, sc
+    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, cuda, fp8=True)
+    plan.route_permute(x, w, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(plan.topk_ids, ids) and torch.equal(plan.pair_row, p["pair_row"])
+    assert torch.equal(plan.xg, p["xg"]) and torch.equal(plan.scales, p["scales"])
 
 
 def test_full_size_deterministic(cuda):
