@@ -104,7 +104,10 @@ int moe_topk(const float* logits, const float* bias, int T, int E, int k,
  * w_dtype BF16: w is [E,H] bf16.  w_dtype FP32: w is [E,H] fp32 and is split
  * into bf16 hi/lo on the device (wsplit_kernel K:1786-1824) so the bf16 GEMM
  * yields fp32-accurate logits.  logits [T,E] fp32 (the reference's
- * router_logits output), counts may be NULL. */
+ * router_logits output), counts may be NULL.  With bf16 weights at E = 256,
+ * H = 7168 or E = 128, H = 2048 the GEMM and the scoring are one kernel
+ * (unless a group-limited rule's groups are not multiples of 32 experts at
+ * E = 256, 16 at E = 128: then the two-kernel path, same results). */
 int moe_route(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
               int E, int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids,
               float* topk_w, int32_t* counts, void* ws, size_t ws_bytes, void* stream);
@@ -158,9 +161,9 @@ int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int
  * out_dtype BF16 or FP8E4M3FN; xg NULL = index only), with the same outputs
  * bit for bit as the two calls.  Replaces run()'s sequence K:4323-4431
  * (wsplit, router GEMM, topk_kernel, offsets_kernel, dispatch and gather).
- * Where the route is one fused kernel (bf16 weights, E = 256 with H = 7168 or
- * E = 128 with H = 2048) and k divides 256 with 256 / k tokens fitting its
- * token tile (k in {2, 4, 8} at E = 256, {4, 8} at E = 128), that kernel's
+ * Where the route is one fused kernel (see moe_route) and k divides 256 with
+ * 256 / k tokens fitting its token tile (k in {2, 4, 8} at E = 256, {4, 8}
+ * at E = 128), that kernel's
  * epilogue writes the permute's per-block expert histograms into the
  * workspace and the permute's histogram launch is skipped; otherwise the two
  * stages run as moe_route and moe_permute would.  counts: the permute's.
