@@ -94,12 +94,14 @@ constexpr int route_fused_lds(int BM, int E, int D) {
 // registers; x is shared through the LDS ring.  D: K steps of loads in
 // flight.  KTC: the K steps, fully unrolled.  V, KK, SC: the scoring lane
 // width, k (0: runtime) and rule.  NTOK: tokens one lane group scores per pass.
+// nt_from: the first tile whose x loads are non-temporal (rf_temporal_tiles).
 template <int BM, int E, int NWV, int D, int KTC, int V, int KK, int SC, int NTOK>
 __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     const __bf16* __restrict__ x, const __bf16* __restrict__ wf, const float* __restrict__ bias,
     int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
     float norm_min, float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ wout,
-    int* __restrict__ counts, int* __restrict__ blockcnt, int nblk, int pt_log2) {
+    int* __restrict__ counts, int* __restrict__ blockcnt, int nblk, int pt_log2,
+    int nt_from) {
   using namespace rf;
   constexpr int NT = 64 * NWV;             // threads
   constexpr int FM = BM / 16;              // 16-row fragments per K half
@@ -140,7 +142,12 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
 #pragma unroll
     for (int q = 0; q < NX; ++q) {
       auto* dst = (__attribute__((address_space(3))) void*)(st + (wave * NX + q) * 1024);
-      __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + src_kt * BK), dst, 16, 0, 0);
+      // tiles from nt_from on: non-temporal (aux bit 1: nt), so they do not
+      // displace the rows of the earlier tiles from the memory-side cache
+      if ((int)blockIdx.x >= nt_from)
+        __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + src_kt * BK), dst, 16, 0, 2);
+      else
+        __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + src_kt * BK), dst, 16, 0, 0);
     }
   };
   bf16x8 wr[D][NWF];
@@ -365,6 +372,22 @@ bool route_fused_block_hist_supported(int E, int k) {
 
 size_t route_fused_workspace_bytes(int E, int H) { return (size_t)E * H * 2; }
 
+// Memory-side cache (MALL, 256 MiB on MI355X) policy for the x stream.  The
+// permute's gather reads x again right after this kernel, token by token.
+// With every x load temporal, the MALL ends up holding the last-read K columns
+// of every token, and the gather's own misses evict them before it gets there.
+// Instead, the tiles of the first kRfMallBytes of x (in token order) load
+// temporal and the rest non-temporal, so the MALL keeps whole rows of the
+// tokens the gather reads first.  Measured at the DeepSeek-V3 shape (C4 step,
+// 5 runs of 20 steps each): 1.700 ms all temporal, 1.709 all non-temporal,
+// 1.681 / 1.679 / 1.678 / 1.680 with the first 100 / 104 / 109 / 114 tiles of
+// 128 tokens temporal (184-210 MB), 1.690 with 80, 1.685 with 120.
+constexpr long long kRfMallBytes = 192ll << 20;
+static int rf_temporal_tiles(int BM, int H) {
+  const long long t = kRfMallBytes / ((long long)BM * H * 2);
+  return t > (1 << 30) ? (1 << 30) : (int)t;
+}
+
 template <int BM, int E, int KTC, int V, int KK, int SC>
 static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias, int T, int H,
                             int k, int renorm, int n_group, int topk_group, float route_scale,
@@ -381,7 +404,7 @@ static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias
   const int nblk = dispatch_blocks((long long)T * k);
   hipLaunchKernelGGL(kern, dim3((unsigned)((T + BM - 1) / BM)), dim3(64 * kRfWaves), 0, s, x, wf,
                      bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, logits,
-                     ids, wout, counts, blockcnt, nblk, pt_log2);
+                     ids, wout, counts, blockcnt, nblk, pt_log2, rf_temporal_tiles(BM, H));
   return hipGetLastError();
 }
 
