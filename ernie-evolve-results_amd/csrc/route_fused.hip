@@ -19,11 +19,12 @@
 //               w loads share the in-order vmcnt counter: waiting for a
 //               step's weights retires its x stage too, and a wave never has
 //               more than 63 loads in flight (the counter's limit).
-//   epilogue    the 128 x 256 fp32 tile goes through LDS once; 8 lanes per
-//               token (16 at E = 128) score it with the scoring kernel's
-//               per-token routine (bit-identical selection), write
-//               router_logits row by row, the ids and weights, and the
-//               block's expert histogram -- optionally one per 256 (token,
+//   epilogue    the 128 x 256 fp32 tile goes through LDS once; its rows are
+//               copied out to router_logits (1 KB per wavefront store,
+//               non-temporal), then 8 lanes per token (16 at E = 128) score
+//               it with the scoring kernel's per-token routine (bit-identical
+//               selection) and write the ids and weights and the block's
+//               expert histogram -- optionally one per 256 (token,
 //               slot) pairs, the permute's block histograms, so the permute
 //               needs no histogram pass.
 #include "moe_common.h"
@@ -237,6 +238,17 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     }
   __syncthreads();
 
+  // ---- logits: the tile's rows copied out whole, one 16-byte vector per lane
+  // (a wavefront writes 1 KB of consecutive floats), non-temporal so they do
+  // not take memory-side cache space from x; issued before the scoring, which
+  // runs while they drain
+  for (int idx = threadIdx.x; idx < BM * (E / 4); idx += NT) {
+    const int row = idx / (E / 4), c4 = idx - row * (E / 4);
+    if (m0 + row < T)
+      __builtin_nontemporal_store(*reinterpret_cast<const f32x4*>(tile + row * TILE_LD + c4 * 4),
+                                  reinterpret_cast<f32x4*>(logits + (m0 + row) * E + c4 * 4));
+  }
+
   // ---- scoring: G = E/V lanes per token
   constexpr int G = E / V;
   constexpr int TPP = NT / G;  // tokens per pass
@@ -274,12 +286,6 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
         l[n][j] = v[0]; l[n][j + 1] = v[1]; l[n][j + 2] = v[2]; l[n][j + 3] = v[3];
       }
       valid[n] = t < T;
-      if (valid[n]) {
-#pragma unroll
-        for (int j = 0; j < V; j += 4)
-          *reinterpret_cast<f32x4*>(logits + t * E + e0 + j) =
-              (f32x4){l[n][j], l[n][j + 1], l[n][j + 2], l[n][j + 3]};
-      }
     }
     int my_id[NTOK];
     float wv[NTOK];
@@ -378,11 +384,14 @@ size_t route_fused_workspace_bytes(int E, int H) { return (size_t)E * H * 2; }
 // of every token, and the gather's own misses evict them before it gets there.
 // Instead, the tiles of the first kRfMallBytes of x (in token order) load
 // temporal and the rest non-temporal, so the MALL keeps whole rows of the
-// tokens the gather reads first.  Measured at the DeepSeek-V3 shape (C4 step,
-// 5 runs of 20 steps each): 1.700 ms all temporal, 1.709 all non-temporal,
-// 1.681 / 1.679 / 1.678 / 1.680 with the first 100 / 104 / 109 / 114 tiles of
-// 128 tokens temporal (184-210 MB), 1.690 with 80, 1.685 with 120.
-constexpr long long kRfMallBytes = 192ll << 20;
+// tokens the gather reads first; the logits go out non-temporal, so they take
+// none of it.  Measured at the DeepSeek-V3 shape (C4 step, 5 runs of 20 steps
+// each, 128-token tiles): all temporal 1.700 ms, all non-temporal 1.709; with
+// the logits stored temporal from registers, the first 100 / 109 / 120 tiles
+// temporal 1.681 / 1.678 / 1.685; with the non-temporal row copy of the
+// logits, 109 / 120 / 130 / 140 / 150 / 160 tiles 1.675 / 1.675 / 1.669 /
+// 1.672 / 1.685 / 1.695.
+constexpr long long kRfMallBytes = 228ll << 20;
 static int rf_temporal_tiles(int BM, int H) {
   const long long t = kRfMallBytes / ((long long)BM * H * 2);
   return t > (1 << 30) ? (1 << 30) : (int)t;
