@@ -248,6 +248,58 @@ def ceiling_bench(c, dev, reps):
           flush=True)
 
 
+def route_floor_bench(c, dev, reps):
+    """What bounds the fused route kernel's K loop: the loop alone and with parts
+    taken out (moe_route_probe, E = 256 and H = 7168 only), beside the real route
+    stage and a plain read of x, all back to back on the same buffers.  Prints
+    one JSON line; `loop_logits_bitexact` checks that the whole-loop probe
+    computes moe_route's logits."""
+    if (c.E, c.H) != (256, 7168):
+        raise SystemExit("--route-floor needs the E = 256, H = 7168 shape (C4 or C5)")
+    x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
+    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, dev, fp8=c.fp8)
+    L = M.lib()
+    stream = M._stream(x)
+    P = M._ptr
+    ws = torch.empty(c.E * c.H * 2, dtype=torch.uint8, device=dev)
+    probe_logits = torch.empty(c.T, c.E, dtype=torch.float32, device=dev)
+    names = ["loop", "mfma_only", "lds_mfma", "x_only", "w_only", "x_from_l2"]
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+
+    def timed(f):
+        # `reps` calls back to back between two events, per call; median of 5
+        ts = []
+        for _ in range(6):
+            a, b = ev(), ev()
+            a.record()
+            for _ in range(reps):
+                f()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3 / reps)
+        return round(statistics.median(ts[1:]), 1)
+
+    plan.route(x, w, bias)
+    M._check(L.moe_route_probe(0, P(x), P(w), c.T, c.H, c.E, P(probe_logits), P(ws), ws.numel(),
+                               stream))
+    torch.cuda.synchronize()
+    exact = bool(torch.equal(probe_logits, plan.logits))
+    out = {}
+    for v, name in enumerate(names):
+        out[name] = timed(lambda: M._check(L.moe_route_probe(v, P(x), P(w), c.T, c.H, c.E, None,
+                                                            P(ws), ws.numel(), stream)))
+    out["route_stage"] = timed(lambda: plan.route(x, w, bias))
+    nx = c.T * c.H * 2 // 16
+    out["x_read"] = timed(lambda: M._check(L.moe_stream_probe(0, P(x), P(plan.out), nx, 1,
+                                                              stream)))
+    mfma_pf = 2.0 * c.T * c.H * c.E / (out["mfma_only"] * 1e-6) / 1e15
+    print(json.dumps({"mode": "route_floor", "config": c.name, "reps": reps,
+                      "note": "us per call, calls back to back; probes and route_stage "
+                              "(moe_route) include the 4-5 us weight re-layout launch",
+                      "us": out, "mfma_only_pflops": round(mfma_pf, 3),
+                      "loop_logits_bitexact": exact}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -265,6 +317,9 @@ def main():
     ap.add_argument("--ceiling", action="store_true",
                     help="time plain streaming kernels that move each stage's byte mix "
                          "(moe_stream_probe) beside the real stages, on the same buffers")
+    ap.add_argument("--route-floor", action="store_true",
+                    help="time the fused route kernel's K loop alone and with parts taken out "
+                         "(moe_route_probe) beside the real route stage")
     ap.add_argument("--layer", nargs="*", type=int, default=None,
                     help="time run() at the reference's workload T values (default: its mix)")
     ap.add_argument("--layer-fp8", action="store_true",
@@ -289,6 +344,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.ceiling:
         ceiling_bench(c, dev, max(args.steps, 5))
+        return
+    if args.route_floor:
+        route_floor_bench(c, dev, max(args.steps, 5))
         return
     x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
     # The router takes bf16 hidden states (K:4327-4339); an fp32 config (C1)

@@ -619,6 +619,25 @@ int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float sca
                   "quant_rows_i8");
 }
 
+int moe_route_probe(int variant, const void* x, const void* w, int T, int H, int E,
+                    float* logits, void* ws, size_t ws_bytes, void* stream) {
+  if (variant < MOE_RPROBE_LOOP || variant > MOE_RPROBE_X_L2)
+    return fail(MOE_ERR_INVALID_ARG, "unknown route probe variant %d", variant);
+  if (E != 256 || H != 7168)
+    return fail(MOE_ERR_UNSUPPORTED, "route probes run the E = 256, H = 7168 loop only (E=%d, H=%d)",
+                E, H);
+  if (T < 1 || T > (1 << 24)) return fail(MOE_ERR_INVALID_ARG, "T=%d not in [1, 2^24]", T);
+  if (!x || !w) return fail(MOE_ERR_NULL_POINTER, "x and w are required");
+  const size_t need = moe::route_fused_workspace_bytes(E, H);
+  if (!ws || ws_bytes < need)
+    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(ws))
+    return fail(MOE_ERR_ALIGNMENT, "x, w and ws must be 16-byte aligned");
+  return launched(moe::launch_route_probe(variant, (const __bf16*)x, (const __bf16*)w, T, H, E,
+                                          logits, ws, (hipStream_t)stream),
+                  "route_probe");
+}
+
 int moe_stream_probe(int pattern, const void* src, void* dst, long long nvec, int ways,
                      void* stream) {
   const int base = pattern & ~MOE_PROBE_GRID_STRIDE;

@@ -60,6 +60,9 @@ hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bia
                               float route_scale, float norm_min, float* logits, int32_t* ids,
                               float* wout, int32_t* counts, int32_t* blockcnt, void* ws,
                               hipStream_t s);
+// K-loop probes of the fused route kernel (E = 256, H = 7168), variants 0-5.
+hipError_t launch_route_probe(int variant, const __bf16* x, const __bf16* w, int T, int H, int E,
+                              float* logits, void* ws, hipStream_t s);
 hipError_t launch_offsets(const int32_t* counts, int E, int32_t* offsets, hipStream_t s);
 hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
                                  int32_t* totals, int32_t* row_token, int32_t* pair_row,

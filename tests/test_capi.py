@@ -359,6 +359,21 @@ def test_stream_probe_validation():
     assert L.moe_stream_probe(1, None, FAKE, 0, 1, None) == 0
 
 
+def test_route_probe_validation():
+    L = M.lib()
+    ws = 256 * 7168 * 2
+    err(L.moe_route_probe(6, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws, None), -2, "variant")
+    err(L.moe_route_probe(-1, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws, None), -2, "variant")
+    err(L.moe_route_probe(0, FAKE, FAKE, 128, 4096, 256, None, FAKE, ws, None), -3, "7168")
+    err(L.moe_route_probe(0, FAKE, FAKE, 128, 7168, 128, None, FAKE, ws, None), -3, "7168")
+    err(L.moe_route_probe(0, FAKE, FAKE, 0, 7168, 256, None, FAKE, ws, None), -2)
+    err(L.moe_route_probe(0, None, FAKE, 128, 7168, 256, None, FAKE, ws, None), -1)
+    err(L.moe_route_probe(0, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws - 1, None), -4)
+    err(L.moe_route_probe(0, FAKE, FAKE, 128, 7168, 256, None, None, ws, None), -4)
+    err(L.moe_route_probe(0, ctypes.c_void_p(0x10008), FAKE, 128, 7168, 256, None, FAKE, ws,
+                          None), -6)
+
+
 def test_route_permute_workspace_and_validation():
     """moe_route_permute: workspace = the route's (rounded up to 256 bytes)
     then the permute's; every argument of both stages is checked before any
