@@ -206,6 +206,11 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
         __builtin_amdgcn_s_barrier();
       }
       const char* sb = lds + (kt % NS) * STAGE_B;
+      // refill x first: stage kt + D goes to the slot of stage kt - 1, which
+      // every wave finished reading before this step's barrier, so its DMA can
+      // start before this step's fragment reads and MFMAs
+      const int kn = kt + D < KT ? kt + D : KT - 1;
+      if constexpr (!(PROBE & RP_NO_X)) issue_x(kt + D, kn);
       // rows i*16 + fr share the swizzle of fr: a half step's FM fragment
       // reads are 2 KB apart
       auto frag_addr = [&](int kk) {
@@ -247,10 +252,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
           }
         }
       }
-      // refill: x stage kt + D goes to the slot of stage kt - 1, which every
-      // wave finished reading before this step's barrier
-      const int kn = kt + D < KT ? kt + D : KT - 1;
-      if constexpr (!(PROBE & RP_NO_X)) issue_x(kt + D, kn);
+      // refill the weights of step kt + D once this step's MFMAs have read them
       if constexpr (!(PROBE & RP_NO_W)) issue_w(kn, wr[u]);
     }
   }
