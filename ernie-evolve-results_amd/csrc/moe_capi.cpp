@@ -146,8 +146,18 @@ static bool route_is_fused(int T, int H, int E, int w_dtype, const moe_route_cfg
          moe::route_fused_supported(E, H, cfg->scoring, cfg->n_group);
 }
 
-// The route's launches over validated arguments.  blockcnt (fused path only,
-// else NULL): also write the permute's raw block histograms.
+// Whether route_launch can also write the permute's block histograms: the
+// fused kernel's tile, or the scoring kernel's block, covers whole blocks of
+// kPairsPerBlock (token, slot) pairs.
+static bool route_block_hist(int T, int H, int E, int k, int w_dtype, const moe_route_cfg* cfg) {
+  if (T == 0) return false;
+  if (route_is_fused(T, H, E, w_dtype, cfg)) return moe::route_fused_block_hist_supported(E, k);
+  return moe::topk_block_hist_supported(E, k, cfg->scoring, cfg->n_group);
+}
+
+// The route's launches over validated arguments.  blockcnt (or NULL; see
+// route_block_hist): also write the permute's raw block histograms, from the
+// fused kernel's epilogue or from the scoring kernel.
 static int route_launch(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
                         int E, int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids,
                         float* topk_w, int32_t* counts, int32_t* blockcnt, void* ws,
@@ -155,7 +165,8 @@ static int route_launch(const void* x, const void* w, int w_dtype, const float* 
   if (T == 0)
     return launched(moe::launch_topk(nullptr, 1, bias, 0, E, k, cfg->scoring, cfg->renormalize,
                                      cfg->n_group, cfg->topk_group, cfg->route_scale,
-                                     cfg->norm_min, nullptr, topk_ids, topk_w, counts, s),
+                                     cfg->norm_min, nullptr, topk_ids, topk_w, counts, nullptr,
+                                     s),
                     "topk");
   if (route_is_fused(T, H, E, w_dtype, cfg))
     return launched(moe::launch_route_fused((const __bf16*)x, (const __bf16*)w, bias, T, E, H, k,
@@ -186,7 +197,7 @@ static int route_launch(const void* x, const void* w, int w_dtype, const float* 
   return launched(moe::launch_topk(gout, parts, bias, T, E, k, cfg->scoring, cfg->renormalize,
                                    cfg->n_group, cfg->topk_group, cfg->route_scale,
                                    cfg->norm_min, parts > 1 ? logits : nullptr, topk_ids, topk_w,
-                                   counts, s),
+                                   counts, blockcnt, s),
                   "topk");
 }
 
@@ -216,7 +227,7 @@ int moe_topk(const float* logits, const float* bias, int T, int E, int k,
   if (logits && !aligned16(logits)) return fail(MOE_ERR_ALIGNMENT, "logits not 16-byte aligned");
   return launched(moe::launch_topk(logits, 1, bias, T, E, k, cfg->scoring, cfg->renormalize,
                                    cfg->n_group, cfg->topk_group, cfg->route_scale,
-                                   cfg->norm_min, nullptr, topk_ids, topk_w, counts,
+                                   cfg->norm_min, nullptr, topk_ids, topk_w, counts, nullptr,
                                    (hipStream_t)stream),
                   "topk");
 }
@@ -409,12 +420,11 @@ int moe_route_permute(const void* x, const void* w, int w_dtype, const float* bi
     return rc;
   hipStream_t s = (hipStream_t)stream;
   void* pws = (char*)ws + rneed;
-  // Where the route is the fused kernel, it writes the permute's block
-  // histograms in its epilogue and the histogram launch is skipped.  The
-  // route never writes counts here: the index kernel writes them from the
-  // scanned totals.
-  const bool handoff = route_is_fused(T, H, E, w_dtype, cfg) &&
-                       moe::route_fused_block_hist_supported(E, k);
+  // Where the route's fused kernel (its epilogue) or its scoring kernel covers
+  // whole permute blocks, it writes the permute's block histograms and the
+  // histogram launch is skipped.  The route never writes counts here: the
+  // index kernel writes them from the scanned totals.
+  const bool handoff = route_block_hist(T, H, E, k, w_dtype, cfg);
   rc = route_launch(x, w, w_dtype, bias, T, H, E, k, cfg, logits, topk_ids, topk_w, nullptr,
                     handoff ? (int32_t*)pws : nullptr, ws, s);
   if (rc) return rc;

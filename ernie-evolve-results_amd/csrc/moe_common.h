@@ -43,10 +43,13 @@ hipError_t launch_wsplit(const float* w, __bf16* wpk, int E, int H, hipStream_t 
 hipError_t launch_router_gemm(const __bf16* x, const __bf16* w, int T, int H, int N,
                               int ksplit, float* out, hipStream_t s);
 int router_gemm_ksplit(int T, int H, int N);
+// blockcnt (or NULL; needs topk_block_hist_supported): also the permute's raw
+// block histograms [E, dispatch_blocks(T*k)], every entry written.
 hipError_t launch_topk(const float* logits, int nparts, const float* bias, int T, int E, int k,
                        int scoring, int renorm, int n_group, int topk_group, float route_scale,
                        float norm_min, float* logits_out, int32_t* ids, float* w,
-                       int32_t* counts, hipStream_t s);
+                       int32_t* counts, int32_t* blockcnt, hipStream_t s);
+bool topk_block_hist_supported(int E, int k, int scoring, int n_group);
 // Router GEMM + scoring in one kernel (E = 256, H = 7168 or E = 128, H = 2048,
 // 16 experts per scoring lane); ws holds route_fused_workspace_bytes(E, H) bytes.
 bool route_fused_supported(int E, int H, int scoring, int n_group);

@@ -16,33 +16,38 @@
 //
 // The histogram is an LDS atomic per selected pair, flushed with one global
 // atomic per expert per block (K:1912-1919).  Integer atomics commute, so the
-// counts are deterministic.
+// counts are deterministic.  With blockcnt, a block scores the 256 / k tokens
+// of one of the permute's blocks of 256 (token, slot) pairs (NPASS passes of
+// its tokens per pass) and also writes that block's expert histogram, every
+// entry, so the permute needs no histogram launch.
 #include "score_token.h"
 
 namespace moe {
 
-// One token per G = E/V lanes; V contiguous experts per lane; 256 threads,
-// one pass: 4 * 64/G tokens per block.
-template <int E, int V, int KK, int SC>
-__global__ __launch_bounds__(256) void topk_kernel(
+// One token per G = E/V lanes; V contiguous experts per lane; NT threads,
+// (NT / 64) * (64 / G) tokens per pass, npass passes (1 without blockcnt).
+template <int E, int V, int KK, int SC, int NT>
+__global__ __launch_bounds__(NT) void topk_kernel(
     const float* __restrict__ logits, int nparts, const float* __restrict__ bias, int T, int k_rt,
     int renorm, int n_group, int topk_group, float route_scale, float norm_min,
     float* __restrict__ lout, int* __restrict__ ids, float* __restrict__ wout,
-    int* __restrict__ counts) {
+    int* __restrict__ counts, int* __restrict__ blockcnt, int nblk, int npass) {
 #pragma clang fp contract(off)
   constexpr int G = E / V;
-  constexpr int TPB = 4 * (64 / G);
+  constexpr int TPB = (NT / 64) * (64 / G);
   static_assert(G >= 8 && G <= 64 && V >= 1 && V <= 16, "lane shape");
   const int k = KK > 0 ? KK : k_rt;  // compile-time for the common k: the rounds unroll
   __shared__ int hist[E];
   const int tid = threadIdx.x;
-  if (counts) {
-    for (int i = tid; i < E; i += 256) hist[i] = 0;
+  const bool hists = counts || blockcnt;
+  if (hists) {
+    for (int i = tid; i < E; i += NT) hist[i] = 0;
     __syncthreads();
   }
 
   const int gl = tid % G;
-  const long long t = (long long)blockIdx.x * TPB + tid / G;
+  for (int pass = 0; pass < npass; ++pass) {
+  const long long t = ((long long)blockIdx.x * npass + pass) * TPB + tid / G;
   const bool valid = t < T;
   const int e0 = gl * V;
   float l[V];
@@ -78,14 +83,17 @@ __global__ __launch_bounds__(256) void topk_kernel(
     if (valid && gl < k) {
       ids[t * k + gl] = my_id;
       wout[t * k + gl] = wv;
-      if (counts) atomicAdd(&hist[my_id], 1);
+      if (hists) atomicAdd(&hist[my_id], 1);
     }
   }
-  if (counts) {
+  }
+  if (hists) {
     __syncthreads();
-    for (int i = tid; i < E; i += 256) {
+    for (int i = tid; i < E; i += NT) {
       const int c = hist[i];
-      if (c) atomicAdd(counts + i, c);
+      if (counts && c) atomicAdd(counts + i, c);
+      // [E, nblk]: this block is the permute's block blockIdx.x
+      if (blockcnt) blockcnt[(long long)i * nblk + blockIdx.x] = c;
     }
   }
 }
@@ -99,19 +107,30 @@ template <int E, int V>
 static hipError_t launch_topk_ev(const float* logits, int nparts, const float* bias, int T, int k,
                                  int scoring, int renorm, int n_group, int topk_group,
                                  float route_scale, float norm_min, float* lout, int32_t* ids,
-                                 float* w, int32_t* counts, hipStream_t s) {
-  constexpr int TPB = 4 * (64 / (E / V));
-  const dim3 grid((unsigned)((T + TPB - 1) / TPB));
+                                 float* w, int32_t* counts, int32_t* blockcnt, hipStream_t s) {
+  constexpr int TPB = 4 * (64 / (E / V));  // tokens per 256 threads
+  // with blockcnt: one block per permute block of kPairsPerBlock pairs, as one
+  // pass of up to 1024 threads, else in passes of 1024
+  const int per_block = kPairsPerBlock / k;  // tokens
+  const int npass = !blockcnt ? 1 : (per_block > 4 * TPB ? per_block / (4 * TPB) : 1);
+  const int nblk = dispatch_blocks((long long)T * k);
+  const dim3 grid((unsigned)(blockcnt ? nblk : (T + TPB - 1) / TPB));
+  const int nt = !blockcnt ? 256 : (per_block >= 4 * TPB ? 1024 : per_block / TPB * 256);
 #define MOE_TOPK_ARGS                                                                      \
-  grid, dim3(256), 0, s, logits, nparts, bias, T, k, renorm, n_group, topk_group, \
-      route_scale, norm_min, lout, ids, w, counts
+  grid, dim3(nt), 0, s, logits, nparts, bias, T, k, renorm, n_group, topk_group, \
+      route_scale, norm_min, lout, ids, w, counts, blockcnt, nblk, npass
+#define MOE_TOPK_NT(KV, SC)                                                      \
+  if (nt == 1024) hipLaunchKernelGGL((topk_kernel<E, V, KV, SC, 1024>), MOE_TOPK_ARGS); \
+  else if (nt == 512) hipLaunchKernelGGL((topk_kernel<E, V, KV, SC, 512>), MOE_TOPK_ARGS); \
+  else hipLaunchKernelGGL((topk_kernel<E, V, KV, SC, 256>), MOE_TOPK_ARGS);
 #define MOE_TOPK_K(SC)                                        \
-  if (k == 8)                                                 \
-    hipLaunchKernelGGL((topk_kernel<E, V, 8, SC>), MOE_TOPK_ARGS); \
-  else if (k == 2)                                            \
-    hipLaunchKernelGGL((topk_kernel<E, V, 2, SC>), MOE_TOPK_ARGS); \
-  else                                                        \
-    hipLaunchKernelGGL((topk_kernel<E, V, 0, SC>), MOE_TOPK_ARGS);
+  if (k == 8) {                                               \
+    MOE_TOPK_NT(8, SC)                                        \
+  } else if (k == 2) {                                        \
+    MOE_TOPK_NT(2, SC)                                        \
+  } else {                                                    \
+    MOE_TOPK_NT(0, SC)                                        \
+  }
   if (scoring == kScoreSoftmax) {
     MOE_TOPK_K(kScoreSoftmax)
   } else if (scoring == kScoreSigmoidGroup) {
@@ -120,6 +139,7 @@ static hipError_t launch_topk_ev(const float* logits, int nparts, const float* b
     MOE_TOPK_K(kScoreSoftmaxBias)
   }
 #undef MOE_TOPK_K
+#undef MOE_TOPK_NT
 #undef MOE_TOPK_ARGS
   return hipGetLastError();
 }
@@ -137,10 +157,16 @@ int topk_lane_width(int E, int scoring, int n_group) {
   return V < 1 ? 1 : V;
 }
 
+bool topk_block_hist_supported(int E, int k, int scoring, int n_group) {
+  if (k < 1 || k > 8 || kPairsPerBlock % k != 0) return false;
+  const int tpb = 4 * (64 / (E / topk_lane_width(E, scoring, n_group)));
+  return (kPairsPerBlock / k) % tpb == 0;
+}
+
 hipError_t launch_topk(const float* logits, int nparts, const float* bias, int T, int E, int k,
                        int scoring, int renorm, int n_group, int topk_group, float route_scale,
                        float norm_min, float* lout, int32_t* ids, float* w, int32_t* counts,
-                       hipStream_t s) {
+                       int32_t* blockcnt, hipStream_t s) {
   if (counts) {
     hipLaunchKernelGGL(zero_i32_kernel, dim3((E + 255) / 256), dim3(256), 0, s, counts, E);
     const hipError_t err = hipGetLastError();
@@ -151,7 +177,8 @@ hipError_t launch_topk(const float* logits, int nparts, const float* bias, int T
 #define MOE_TOPK_CASE(EE, VV)                                                               \
   if (E == EE && V == VV)                                                                   \
     return launch_topk_ev<EE, VV>(logits, nparts, bias, T, k, scoring, renorm, n_group,       \
-                                  topk_group, route_scale, norm_min, lout, ids, w, counts, s);
+                                  topk_group, route_scale, norm_min, lout, ids, w, counts,    \
+                                  blockcnt, s);
   MOE_TOPK_CASE(8, 1)
   MOE_TOPK_CASE(16, 2)
   MOE_TOPK_CASE(32, 2)

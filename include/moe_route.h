@@ -161,12 +161,15 @@ int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int
  * out_dtype BF16 or FP8E4M3FN; xg NULL = index only), with the same outputs
  * bit for bit as the two calls.  Replaces run()'s sequence K:4323-4431
  * (wsplit, router GEMM, topk_kernel, offsets_kernel, dispatch and gather).
- * Where the route is one fused kernel (see moe_route) and k divides 256 with
- * 256 / k tokens fitting its token tile (k in {2, 4, 8} at E = 256, {4, 8}
- * at E = 128), that kernel's
- * epilogue writes the permute's per-block expert histograms into the
- * workspace and the permute's histogram launch is skipped; otherwise the two
- * stages run as moe_route and moe_permute would.  counts: the permute's.
+ * Where a route kernel covers whole permute blocks of 256 (token, slot)
+ * pairs, it also writes the permute's per-block expert histograms into the
+ * workspace and the permute's histogram launch is skipped: the fused kernel
+ * (see moe_route) when 256 / k tokens fit its token tile (k in {2, 4, 8} at
+ * E = 256, {4, 8} at E = 128), else the scoring kernel when 256 / k is a
+ * multiple of the tokens one of its passes scores (k in {1, 2, 4, 8}: 32
+ * tokens per pass at E <= 128, 16 at E = 256, fewer with expert groups
+ * narrower than 16); otherwise the
+ * two stages run as moe_route and moe_permute would.  counts: the permute's.
  * ws: moe_route_permute_workspace_bytes(T, H, E, k, w_dtype) bytes, 16-byte
  * aligned (the route's workspace, rounded up to 256 bytes, then the
  * permute's).  Every argument of both stages is checked before any launch. */

@@ -5,11 +5,13 @@ pair_row, offsets, counts).
 
 Where the route is the fused kernel and k divides 256 with 256 / k tokens
 fitting its token tile (E = 256: k in {2, 4, 8}; E = 128: k in {4, 8}), the
-fused kernel's epilogue writes the permute's block histograms, so these
-cases check that handoff: token counts that end inside a block of 256 pairs
-and inside a route tile (1, 33, 129, 1000, 4133), k = 5 and k = 1 (no
-handoff), an unfused shape (E = 64) and fp32 weights (the hi/lo split
-route of the reference's run() shape).  Needs an MI355X."""
+fused kernel's epilogue writes the permute's block histograms; on the
+two-kernel route (other shapes, fp32 weights) the scoring kernel writes them
+when k divides 256.  These cases check both handoffs: token counts that end
+inside a block of 256 pairs and inside a route tile (1, 33, 129, 1000,
+4133), k = 5, 3 and (fused) 1 (no handoff), unfused shapes from E = 8 to
+E = 256, C2's split-K GEMM and fp32 weights (the hi/lo split route of the
+reference's run() shape).  Needs an MI355X."""
 import ctypes
 
 import pytest
@@ -115,8 +117,16 @@ CASES = [
     (128, 2048, 8, 4133, True, False),
     (128, 2048, 4, 1000, False, False),    # 64-token blocks = one tile
     (128, 2048, 2, 200, False, False),     # no handoff: 128-token blocks > tile
-    (64, 1024, 8, 1000, False, False),     # unfused route
+    (64, 1024, 8, 1000, False, False),     # unfused route: the scoring kernel's handoff
     (64, 8192, 8, 1571, False, True),      # fp32 weights (hi/lo split): the run() shape
+    (8, 4096, 2, 8192, False, False),      # C2's shape: split-K GEMM, 128-token blocks
+    (8, 1024, 2, 1001, True, False),       # a last block of 18 pairs
+    (16, 512, 1, 300, False, False),       # 256-token blocks, 8 scoring passes
+    (32, 512, 4, 97, False, False),
+    (128, 1024, 8, 333, False, False),     # unfused at E = 128
+    (256, 1024, 8, 555, False, False),     # unfused at E = 256 (sigmoid groups, 16-token passes)
+    (256, 1024, 2, 257, True, False),
+    (64, 1024, 3, 400, False, False),      # no handoff: 256 % 3 != 0
 ]
 
 
