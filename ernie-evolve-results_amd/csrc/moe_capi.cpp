@@ -254,6 +254,17 @@ size_t moe_permute_workspace_bytes(int T, int E, int k) {
   return round256((size_t)E * nblk * 4) + round256((size_t)E * 4);
 }
 
+// The fp8 permute's token-major scale stage, after the permute's workspace.
+static size_t fp8_stage_bytes(int T, int H) {
+  if (T <= 0 || H <= 0 || H % 128 != 0) return 0;
+  return round256((size_t)T * (H / 128) * 4);
+}
+
+size_t moe_permute_fp8_workspace_bytes(int T, int H, int E, int k) {
+  if (T < 0 || H < 0 || E < 0 || k < 0) return 0;
+  return moe_permute_workspace_bytes(T, E, k) + fp8_stage_bytes(T, H);
+}
+
 }  // extern "C"
 
 // Argument checks of moe_permute, everything except the workspace.
@@ -297,10 +308,13 @@ static int check_permute(const void* x, int x_dtype, const int32_t* topk_ids, in
 // moe_permute_workspace_bytes(T, E, k) bytes.
 // hist_ready: the workspace already holds the raw block histograms (written
 // by the fused route kernel), so the histogram launch is skipped; T * k > 0.
+// stage (fp8 with offsets only, else NULL): fp8_stage_bytes(T, H) bytes for
+// the token-major scales.
 static int permute_launch(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H,
                           int E, int k, int out_dtype, void* xg, float* scales,
                           int32_t* row_token, int32_t* pair_row, int32_t* offsets,
-                          int32_t* counts, void* ws, void* stream, bool hist_ready = false) {
+                          int32_t* counts, void* ws, void* stream, bool hist_ready = false,
+                          void* stage = nullptr) {
   const bool fp8 = out_dtype == MOE_DTYPE_FP8E4M3FN;
   const int elem = x_dtype == MOE_DTYPE_BF16 ? 2 : 4;
   hipStream_t s = (hipStream_t)stream;
@@ -315,7 +329,11 @@ static int permute_launch(const void* x, int x_dtype, const int32_t* topk_ids, i
                                                      row_token, pair_row, offsets, counts, s),
                           "dispatch_index");
   if (rc || !xg || T == 0) return rc;
-  if (fp8) return launched(moe::launch_gather_fp8(x, pair_row, T, H, k, xg, scales, s), "gather_fp8");
+  if (fp8)
+    return launched(moe::launch_gather_fp8(x, pair_row, row_token, offsets ? offsets + E : nullptr,
+                                           T, H, k, xg, scales,
+                                           offsets ? (float*)stage : nullptr, s),
+                    "gather_fp8");
   return launched(moe::launch_gather(x, elem, pair_row, T, H, k, xg, s), "gather");
 }
 
@@ -372,8 +390,13 @@ int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int 
   const size_t need = moe_permute_workspace_bytes(T, E, k);
   if (!ws || ws_bytes < need)
     return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
+  // fp8 rows with room for the scale stage after the permute's workspace
+  void* stage = nullptr;
+  if (out_dtype == MOE_DTYPE_FP8E4M3FN && fp8_stage_bytes(T, H) > 0 &&
+      ws_bytes >= moe_permute_fp8_workspace_bytes(T, H, E, k))
+    stage = (char*)ws + need;
   return permute_launch(x, x_dtype, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
-                        pair_row, offsets, counts, ws, stream);
+                        pair_row, offsets, counts, ws, stream, false, stage);
 }
 
 size_t moe_permute_noalloc_max_scratch_bytes(void) { return kNoallocScratchBytes; }
@@ -399,7 +422,7 @@ int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int
 size_t moe_route_permute_workspace_bytes(int T, int H, int E, int k, int w_dtype) {
   if (T < 0 || H < 0 || E <= 0 || k < 0) return 0;
   return round256(moe_route_workspace_bytes(T, H, E, w_dtype)) +
-         moe_permute_workspace_bytes(T, E, k);
+         moe_permute_fp8_workspace_bytes(T, H, E, k);
 }
 
 int moe_route_permute(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
@@ -428,8 +451,10 @@ int moe_route_permute(const void* x, const void* w, int w_dtype, const float* bi
   rc = route_launch(x, w, w_dtype, bias, T, H, E, k, cfg, logits, topk_ids, topk_w, nullptr,
                     handoff ? (int32_t*)pws : nullptr, ws, s);
   if (rc) return rc;
+  void* stage = (char*)pws + moe_permute_workspace_bytes(T, E, k);
   return permute_launch(x, MOE_DTYPE_BF16, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
-                        pair_row, offsets, counts, pws, stream, handoff);
+                        pair_row, offsets, counts, pws, stream, handoff,
+                        fp8_stage_bytes(T, H) > 0 ? stage : nullptr);
 }
 
 int moe_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* topk_w,

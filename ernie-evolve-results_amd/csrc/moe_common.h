@@ -77,8 +77,11 @@ hipError_t launch_dispatch_from_hist(const int32_t* ids, int T, int E, int k, in
                                      int32_t* offsets, int32_t* counts, hipStream_t s);
 hipError_t launch_gather(const void* x, int elem_bytes, const int32_t* pair_row, int T, int H,
                          int k, void* xg, hipStream_t s);
-hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, int T, int H, int k,
-                             void* xg, float* scales, hipStream_t s);
+// stage (or NULL): T * (H/128) fp32 of workspace for the token-major scales,
+// then copied to the destination rows r < *nrows (offsets[E]) through row_token.
+hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, const int32_t* row_token,
+                             const int32_t* nrows, int T, int H, int k, void* xg, float* scales,
+                             float* stage, hipStream_t s);
 hipError_t launch_combine(const void* y, int y_dtype, const int32_t* pair_row, const float* w,
                           const void* shared, int T, int H, int k, void* out, hipStream_t s);
 

@@ -15,6 +15,7 @@
 // s = max(amax, 1e-10) / 448 into all k rows (16 bytes per lane), plus the
 // scale.
 #include "moe_common.h"
+#include <type_traits>
 
 namespace moe {
 
@@ -79,12 +80,19 @@ __device__ __forceinline__ unsigned int cvt_fp8x4(float a, float b, float c, flo
 // store per destination row); the 8 lanes of a 1x128 block reduce |x| max
 // with xor shuffles, and the block's first lane writes the scale -- the 8
 // blocks of a wavefront's 1 KB of fp8 row land as 8 consecutive scales, one
-// 32-byte run per store instruction.
+// 32-byte run per store instruction.  With `stage`, the scale goes once into
+// the token-major stage[t * nb + blk] instead of into the k destination rows
+// (a 256-thread block writes 32 consecutive scales: one whole 128-byte line),
+// and scatter_scales_kernel copies whole destination rows afterwards: the k
+// scattered 32-byte runs per token cost more than the fp8 rows they describe
+// (C5: gather 438 against 403 us and the combine after it 762 against 732 us
+// with and without them).
 __global__ __launch_bounds__(256) void gather_fp8_kernel(const u32x4* __restrict__ x,
                                                          const int* __restrict__ pair_row,
                                                          long long nchunks, int cpr, int nb,
                                                          int k, u32x4* __restrict__ xg,
-                                                         float* __restrict__ scales) {
+                                                         float* __restrict__ scales,
+                                                         float* __restrict__ stage) {
   // chunk c = t * cpr + v: 16 elements of token t; cpr = H / 16 is a multiple
   // of 8, so the 8 lanes of a block share t and leave the loop together
   const int lane8 = threadIdx.x & 7;
@@ -116,22 +124,78 @@ __global__ __launch_bounds__(256) void gather_fp8_kernel(const u32x4* __restrict
       packed[q] = cvt_fp8x4(qv[4 * q], qv[4 * q + 1], qv[4 * q + 2], qv[4 * q + 3]);
     const int* pr = pair_row + (long long)t * k;
     const int blk = v >> 3;
+    if (stage && lane8 == 0) stage[(long long)t * nb + blk] = scale;
     for (int j = 0; j < k; ++j) {
       const int r = pr[j];
       if (r < 0) continue;
       st_nt(xg + (long long)r * cpr + v, packed);
-      if (lane8 == 0) scales[(long long)r * nb + blk] = scale;
+      if (!stage && lane8 == 0) scales[(long long)r * nb + blk] = scale;
     }
   }
 }
 
-hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, int T, int H, int k,
-                             void* xg, float* scales, hipStream_t s) {
+// scales[r] = stage[row_token[r]] for the rows r < offsets[E] that exist, as
+// whole rows in destination order: consecutive lanes write consecutive
+// 16-byte pieces (nb % 4 == 0) or floats, so every store is part of a
+// contiguous run and the lines go out whole.
+// Each thread moves kScatterItems pieces, 256 * gridDim apart (a block's
+// pieces of one round are contiguous), all loads before the stores: the stage
+// is read from L2 or the memory-side cache, and one load in flight per lane
+// left the kernel latency-bound.
+constexpr int kScatterItems = 4;
+template <int W>
+__global__ __launch_bounds__(256) void scatter_scales_kernel(const float* __restrict__ stage,
+                                                             const int* __restrict__ row_token,
+                                                             const int* __restrict__ nrows_p,
+                                                             long long nitems, int nb,
+                                                             float* __restrict__ scales) {
+  using Piece = typename std::conditional<W == 4, u32x4, float>::type;
+  const int per_row = nb / W;
+  const long long nrows = *nrows_p;
+  const long long stride = (long long)gridDim.x * 256;
+  const long long q0 = (long long)blockIdx.x * 256 + threadIdx.x;
+  Piece v[kScatterItems];
+  long long dst[kScatterItems];
+#pragma unroll
+  for (int i = 0; i < kScatterItems; ++i) {
+    const long long q = q0 + i * stride;
+    const long long r = q / per_row;
+    dst[i] = -1;
+    if (q < nitems && r < nrows) {
+      const int p = (int)(q - r * per_row);
+      const long long t = row_token[r];
+      v[i] = reinterpret_cast<const Piece*>(stage + t * nb)[p];
+      dst[i] = r * per_row + p;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kScatterItems; ++i) {
+    if (dst[i] < 0) continue;
+    if constexpr (W == 4) st_nt(reinterpret_cast<u32x4*>(scales) + dst[i], v[i]);
+    else scales[dst[i]] = v[i];
+  }
+}
+
+hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, const int32_t* row_token,
+                             const int32_t* nrows, int T, int H, int k, void* xg, float* scales,
+                             float* stage, hipStream_t s) {
   const int cpr = H / 16;  // 16-element chunks per row (H % 128 == 0: a multiple of 8)
+  const int nb = H / 128;
   const long long nchunks = (long long)T * cpr;
   if (nchunks == 0) return hipSuccess;
   hipLaunchKernelGGL(gather_fp8_kernel, dim3(grid_for(nchunks)), dim3(256), 0, s,
-                     (const u32x4*)x, pair_row, nchunks, cpr, H / 128, k, (u32x4*)xg, scales);
+                     (const u32x4*)x, pair_row, nchunks, cpr, nb, k, (u32x4*)xg, scales, stage);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !stage) return e;
+  const bool vec = nb % 4 == 0;
+  const long long nitems = (long long)T * k * (vec ? nb / 4 : nb);
+  const dim3 sgrid((unsigned)((nitems + 256LL * kScatterItems - 1) / (256LL * kScatterItems)));
+  if (vec)
+    hipLaunchKernelGGL(scatter_scales_kernel<4>, sgrid, dim3(256), 0, s, stage, row_token, nrows,
+                       nitems, nb, scales);
+  else
+    hipLaunchKernelGGL(scatter_scales_kernel<1>, sgrid, dim3(256), 0, s, stage, row_token, nrows,
+                       nitems, nb, scales);
   return hipGetLastError();
 }
 

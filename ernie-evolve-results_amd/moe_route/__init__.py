@@ -36,7 +36,7 @@ EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
            "moe_grouped_gemm_i8", "moe_grouped_swiglu_i8", "moe_grouped_gemm_rows",
            "moe_grouped_swiglu_rows", "moe_permute_noalloc_max_scratch_bytes",
            "moe_permute_noalloc", "moe_stream_probe", "moe_route_permute_workspace_bytes",
-           "moe_route_permute", "moe_route_probe"]
+           "moe_route_permute", "moe_route_probe", "moe_permute_fp8_workspace_bytes"]
 
 
 class MoeError(RuntimeError):
@@ -74,6 +74,8 @@ def lib():
         L.moe_route_workspace_bytes.argtypes = [_I, _I, _I, _I]
         L.moe_permute_workspace_bytes.restype = _Z
         L.moe_permute_workspace_bytes.argtypes = [_I, _I, _I]
+        L.moe_permute_fp8_workspace_bytes.restype = _Z
+        L.moe_permute_fp8_workspace_bytes.argtypes = [_I, _I, _I, _I]
         L.moe_router_gemm.restype = _I
         L.moe_router_gemm.argtypes = [_P, _P, _I, _I, _I, _P, _P]
         L.moe_topk.restype = _I
@@ -283,7 +285,8 @@ def permute(x, topk_ids, E, fp8=False, index_only=False):
     offs = torch.empty(E + 1, dtype=torch.int32, device=dev)
     counts = torch.empty(E, dtype=torch.int32, device=dev)
     L = lib()
-    nws = L.moe_permute_workspace_bytes(T, E, k)
+    nws = (L.moe_permute_fp8_workspace_bytes(T, H, E, k) if fp8 and not index_only
+           else L.moe_permute_workspace_bytes(T, E, k))
     ws = torch.empty(max(nws, 1), dtype=torch.uint8, device=dev)
     _check(L.moe_permute(_ptr(x), xd, _ptr(topk_ids), T, H, E, k, od, _ptr(xg), _ptr(scales),
                          _ptr(row_token), _ptr(pair_row), _ptr(offs), _ptr(counts), _ptr(ws),
@@ -641,7 +644,8 @@ class MoePlan:
         self.out = torch.empty(T, H, dtype=x_dtype, device=dev)  # combine writes y's dtype
         self.nws_route = L.moe_route_workspace_bytes(T, H, E, self.wd)
         self.ws_route = torch.empty(max(self.nws_route, 256), dtype=torch.uint8, device=dev)
-        self.nws_perm = L.moe_permute_workspace_bytes(T, E, k)
+        self.nws_perm = (L.moe_permute_fp8_workspace_bytes(T, H, E, k) if fp8
+                         else L.moe_permute_workspace_bytes(T, E, k))
         self.ws_perm = torch.empty(max(self.nws_perm, 256), dtype=torch.uint8, device=dev)
         # one call for route + permute (bf16 x): the route's and the permute's
         # workspaces back to back

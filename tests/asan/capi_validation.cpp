@@ -64,8 +64,12 @@ int main() {
   {
     moe_route_cfg rc{MOE_SCORING_SOFTMAX, 1, 1, 1, 1.0f, 0.0f};
     const size_t rp = moe_route_permute_workspace_bytes(16, 128, 8, 2, MOE_DTYPE_BF16);
+    // route's workspace (rounded up to 256), the permute's, the fp8 scale stage
+    // (16 tokens x 1 block of 128 fp32, rounded up to 256)
     if (rp != ((moe_route_workspace_bytes(16, 128, 8, MOE_DTYPE_BF16) + 255) / 256) * 256 +
-                  moe_permute_workspace_bytes(16, 8, 2))
+                  moe_permute_workspace_bytes(16, 8, 2) + 256)
+      ++failures;
+    if (moe_permute_fp8_workspace_bytes(16, 128, 8, 2) != moe_permute_workspace_bytes(16, 8, 2) + 256)
       ++failures;
     EXPECT(moe_route_permute(fake, fake, 0, nullptr, 16, 128, 8, 2, &rc, fp, ip, fp, 0, fake, nullptr, ip, ip, ip, ip, nullptr, rp, nullptr), MOE_ERR_WORKSPACE);
     EXPECT(moe_route_permute(fake, fake, 0, nullptr, 16, 128, 8, 2, &rc, fp, ip, fp, 1, fake, nullptr, ip, ip, ip, ip, fake, rp, nullptr), MOE_ERR_UNSUPPORTED);

@@ -376,15 +376,23 @@ def test_route_probe_validation():
 
 def test_route_permute_workspace_and_validation():
     """moe_route_permute: workspace = the route's (rounded up to 256 bytes)
-    then the permute's; every argument of both stages is checked before any
-    launch."""
+    then the permute's with its fp8 scale stage (T * H/128 fp32, rounded up
+    to 256 bytes, when H % 128 == 0); every argument of both stages is
+    checked before any launch."""
     L = M.lib()
     r256 = lambda n: (n + 255) // 256 * 256
     for (T, H, E, k) in [(32768, 7168, 256, 8), (16384, 2048, 128, 8), (100, 128, 8, 2),
-                         (0, 7168, 256, 8), (4133, 7168, 256, 5)]:
+                         (0, 7168, 256, 8), (4133, 7168, 256, 5), (100, 64, 8, 2)]:
+        stage = r256(T * (H // 128) * 4) if T > 0 and H % 128 == 0 else 0
+        assert L.moe_permute_fp8_workspace_bytes(T, H, E, k) == \
+            L.moe_permute_workspace_bytes(T, E, k) + stage
         assert L.moe_route_permute_workspace_bytes(T, H, E, k, 0) == \
-            r256(L.moe_route_workspace_bytes(T, H, E, 0)) + L.moe_permute_workspace_bytes(T, E, k)
+            r256(L.moe_route_workspace_bytes(T, H, E, 0)) + L.moe_permute_workspace_bytes(T, E, k) \
+            + stage
+    assert L.moe_permute_fp8_workspace_bytes(32768, 7168, 256, 8) - \
+        L.moe_permute_workspace_bytes(32768, 256, 8) == 32768 * 56 * 4
     assert L.moe_route_permute_workspace_bytes(-1, 7168, 256, 8, 0) == 0
+    assert L.moe_permute_fp8_workspace_bytes(-1, 7168, 256, 8) == 0
     c = cfg()
     need = L.moe_route_permute_workspace_bytes(16, 128, 8, 2, 0)
 
