@@ -7,7 +7,7 @@
 // are ranked by their flat index t*k + j, giving exactly
 // argsort(topk_ids.flatten(), stable) -- by expert, then ascending token.
 //
-// Three launches (two when E * blocks <= kSumMax: the index kernel then sums
+// Three launches (two when E * blocks <= kDispatchSumMax: the index kernel then sums
 // the block histograms itself), all integer work over the T*k ids (1 MB at
 // T=32768, k=8):
 //   1. pair_hist:   per block of 256 pairs, one 64-bit LDS bitmask word per
@@ -127,14 +127,16 @@ __device__ __forceinline__ void lds_offsets(const int* __restrict__ cnt, int E, 
   if (tid == 0) offs[E] = total;
 }
 
-// Small problems (E * nblk <= kSumMax): dispatch_index_kernel reads the raw
-// block histograms itself -- each block sums, per expert, the counts of the
-// blocks before it and of all blocks -- so block_scan_kernel is not launched.
+// Small problems (E * ncol <= kDispatchSumMax): dispatch_index_kernel reads
+// the raw block histograms itself -- each block sums, per expert, the counts
+// of the blocks before it and of all blocks -- so block_scan_kernel is not
+// launched.  The histograms may be finer than the index blocks: ncol columns
+// of sub-blocks, sub of them per index block (the small-E route kernel's
+// 32-token tiles), summed the same way.
 // P = 256 / E lanes (a power of two, at most 64) share one expert's column.
-constexpr int kSumMax = 8192;
-
-__device__ __forceinline__ void column_sums(const int* __restrict__ blockcnt, int nblk, int E,
-                                            int* base_out, int* tot_out) {
+constexpr int kColBatch = 8;
+__device__ __forceinline__ void column_sums(const int* __restrict__ blockcnt, int ncol, int sub,
+                                            int E, int* base_out, int* tot_out) {
   const int tid = threadIdx.x;
   int P = 64;
   while (P > 1 && P * E > kPairsPerBlock) P >>= 1;
@@ -143,11 +145,23 @@ __device__ __forceinline__ void column_sums(const int* __restrict__ blockcnt, in
     const int e = e0 + tid / P, j = tid % P;
     int before = 0, all = 0;
     if (tid / P < per && e < E) {
-      const int* col = blockcnt + (long long)e * nblk;
-      for (int i = j; i < nblk; i += P) {
-        const int c = col[i];
-        all += c;
-        if (i < (int)blockIdx.x) before += c;
+      const int* col = blockcnt + (long long)e * ncol;
+      const int first = (int)blockIdx.x * sub;  // this block's first column
+      // kColBatch independent loads per lane before any add: a lane sums up
+      // to ncol / P columns, and one load at a time would pay the memory
+      // latency per column
+      for (int i0 = j; i0 < ncol; i0 += P * kColBatch) {
+        int c[kColBatch];
+#pragma unroll
+        for (int u = 0; u < kColBatch; ++u) {
+          const int i = i0 + u * P;
+          c[u] = i < ncol ? col[i] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kColBatch; ++u) {
+          all += c[u];
+          if (i0 + u * P < first) before += c[u];
+        }
       }
     }
     // reduce over the P lanes of the expert (P divides 64: groups never straddle a wave)
@@ -162,12 +176,13 @@ __device__ __forceinline__ void column_sums(const int* __restrict__ blockcnt, in
   }
 }
 
-// SUM = false: blockbase is block_scan_kernel's scanned columns and totals its
-// per-expert totals.  SUM = true: blockbase is pair_hist_kernel's raw block
-// histograms, summed here (totals unused).
+// SUM = false: blockbase is block_scan_kernel's scanned columns [E, nblk] and
+// totals its per-expert totals.  SUM = true: blockbase is raw histograms
+// [E, ncol], sub columns per block (pair_hist_kernel's: ncol = nblk, sub = 1),
+// summed here (totals unused).
 template <bool SUM>
 __global__ __launch_bounds__(kPairsPerBlock) void dispatch_index_kernel(
-    const int* __restrict__ ids, long long npairs, int E, int k, int nblk,
+    const int* __restrict__ ids, long long npairs, int E, int k, int nblk, int ncol, int sub,
     const int* __restrict__ blockbase, const int* __restrict__ totals,
     int* __restrict__ row_token, int* __restrict__ pair_row, int* __restrict__ offsets_out,
     int* __restrict__ counts_out) {
@@ -179,7 +194,7 @@ __global__ __launch_bounds__(kPairsPerBlock) void dispatch_index_kernel(
   const int tid = threadIdx.x;
   for (int i = tid; i < E * kMaskWords; i += kPairsPerBlock) mask[i] = 0ull;
   if (SUM) {
-    column_sums(blockbase, nblk, E, sbase, stot);
+    column_sums(blockbase, ncol, sub, E, sbase, stot);
     __syncthreads();
     totals = stot;
   }
@@ -246,25 +261,32 @@ hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_
                      npairs, E, nblk, blockcnt);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  return launch_dispatch_from_hist(ids, T, E, k, blockcnt, totals, row_token, pair_row, offsets,
-                                   counts, s);
+  return launch_dispatch_from_hist(ids, T, E, k, blockcnt, 0, totals, row_token, pair_row,
+                                   offsets, counts, s);
 }
 
 // The scan and index launches over raw block histograms already in blockcnt
-// (pair_hist_kernel's, or the fused route kernel's epilogue).  T * k > 0.
+// (pair_hist_kernel's, or a route kernel's epilogue).  sub_tokens = 0: one
+// column per index block, [E, nblk]; else columns of sub_tokens tokens each,
+// [E, ceil(T / sub_tokens)], whole columns per index block (256 / k a multiple
+// of sub_tokens) and few enough for the summing path (dispatch_sum_path).
+// T * k > 0.
 hipError_t launch_dispatch_from_hist(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
-                                     int32_t* totals, int32_t* row_token, int32_t* pair_row,
-                                     int32_t* offsets, int32_t* counts, hipStream_t s) {
+                                     int sub_tokens, int32_t* totals, int32_t* row_token,
+                                     int32_t* pair_row, int32_t* offsets, int32_t* counts,
+                                     hipStream_t s) {
   const long long npairs = (long long)T * k;
   const int nblk = dispatch_blocks(npairs);
   const size_t shm_hist = sizeof(unsigned long long) * E * kMaskWords;
   hipError_t err;
-  if ((long long)E * nblk <= kSumMax) {
+  const int ncol = sub_tokens ? (T + sub_tokens - 1) / sub_tokens : nblk;
+  const int sub = sub_tokens ? kPairsPerBlock / k / sub_tokens : 1;
+  if (sub_tokens || dispatch_sum_path(E, nblk)) {
     // few block histograms: every index block sums them itself, no scan launch
     const size_t shm_sum = shm_hist + sizeof(int) * (3 * E + 1);
     hipLaunchKernelGGL(dispatch_index_kernel<true>, dim3(nblk), dim3(kPairsPerBlock), shm_sum, s,
-                       ids, npairs, E, k, nblk, blockcnt, totals, row_token, pair_row, offsets,
-                       counts);
+                       ids, npairs, E, k, nblk, ncol, sub, blockcnt, totals, row_token, pair_row,
+                       offsets, counts);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(block_scan_kernel, dim3(E), dim3(256), 0, s, blockcnt, nblk, totals);
@@ -272,8 +294,8 @@ hipError_t launch_dispatch_from_hist(const int32_t* ids, int T, int E, int k, in
   if (err != hipSuccess) return err;
   const size_t shm_idx = shm_hist + sizeof(int) * (E + 1);
   hipLaunchKernelGGL(dispatch_index_kernel<false>, dim3(nblk), dim3(kPairsPerBlock), shm_idx, s,
-                     ids, npairs, E, k, nblk, blockcnt, totals, row_token, pair_row, offsets,
-                     counts);
+                     ids, npairs, E, k, nblk, nblk, 1, blockcnt, totals, row_token, pair_row,
+                     offsets, counts);
   return hipGetLastError();
 }
 

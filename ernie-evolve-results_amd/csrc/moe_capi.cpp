@@ -102,6 +102,8 @@ static int route_parts(int T, int H, int E, int w_dtype) {
 size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype) {
   if (T < 0 || H < 0 || E <= 0) return 0;
   if (w_dtype != MOE_DTYPE_BF16 && w_dtype != MOE_DTYPE_FP32) return 0;
+  // E = 8 or 16 with bf16 weights: the small-E GEMM + scoring kernel, no workspace
+  if (w_dtype == MOE_DTYPE_BF16 && moe::route_small_supported(E, H)) return 0;
   const int parts = route_parts(T, H, E, w_dtype);
   size_t b = 0;
   if (w_dtype == MOE_DTYPE_FP32) b += round256((size_t)2 * E * H * 2);
@@ -146,18 +148,55 @@ static bool route_is_fused(int T, int H, int E, int w_dtype, const moe_route_cfg
          moe::route_fused_supported(E, H, cfg->scoring, cfg->n_group);
 }
 
-// Whether route_launch can also write the permute's block histograms: the
-// fused kernel's tile, or the scoring kernel's block, covers whole blocks of
-// kPairsPerBlock (token, slot) pairs.
-static bool route_block_hist(int T, int H, int E, int k, int w_dtype, const moe_route_cfg* cfg) {
-  if (T == 0) return false;
-  if (route_is_fused(T, H, E, w_dtype, cfg)) return moe::route_fused_block_hist_supported(E, k);
-  return moe::topk_block_hist_supported(E, k, cfg->scoring, cfg->n_group);
+// Whether route_launch takes the small-E kernel (E = 8 or 16, bf16 weights,
+// any scoring rule).
+static bool route_is_small(int T, int H, int E, int w_dtype) {
+  return T > 0 && w_dtype == MOE_DTYPE_BF16 && moe::route_small_supported(E, H);
+}
+
+// What the route can hand the permute instead of its histogram launch.
+enum RouteHist {
+  kHistNone,    // nothing: the permute counts its blocks itself
+  kHistBlocks,  // the raw block histograms [E, nblk], at the permute's workspace
+  kHistSub,     // the small-E kernel's 32-token histograms [E, ceil(T/32)], in
+                // route_sub_hist_bytes after the permute's workspace
+};
+
+// kHistSub: every permute block of 256 / k tokens is whole 32-token columns
+// and the columns are few enough for the index kernel to sum them itself.
+static bool route_sub_hist(int T, int H, int E, int k, int w_dtype) {
+  if (!route_is_small(T, H, E, w_dtype)) return false;
+  const int st = moe::route_small_tokens();
+  if (k < 1 || k > 8 || moe::kPairsPerBlock % k != 0 || (moe::kPairsPerBlock / k) % st != 0)
+    return false;
+  return moe::dispatch_sum_path(E, (T + st - 1) / st);
+}
+
+static size_t route_sub_hist_bytes(int T, int H, int E, int k, int w_dtype) {
+  if (!route_sub_hist(T, H, E, k, w_dtype)) return 0;
+  const int st = moe::route_small_tokens();
+  return round256((size_t)E * ((T + st - 1) / st) * 4);
+}
+
+// Which histograms route_launch can also write for the permute: the fused
+// kernel's tile, or the scoring kernel's block, covering whole blocks of
+// kPairsPerBlock (token, slot) pairs, or the small-E kernel's 32-token
+// columns.
+static RouteHist route_block_hist(int T, int H, int E, int k, int w_dtype,
+                                  const moe_route_cfg* cfg) {
+  if (T == 0) return kHistNone;
+  if (route_is_small(T, H, E, w_dtype))
+    return route_sub_hist(T, H, E, k, w_dtype) ? kHistSub : kHistNone;
+  if (route_is_fused(T, H, E, w_dtype, cfg))
+    return moe::route_fused_block_hist_supported(E, k) ? kHistBlocks : kHistNone;
+  return moe::topk_block_hist_supported(E, k, cfg->scoring, cfg->n_group) ? kHistBlocks
+                                                                           : kHistNone;
 }
 
 // The route's launches over validated arguments.  blockcnt (or NULL; see
 // route_block_hist): also write the permute's raw block histograms, from the
-// fused kernel's epilogue or from the scoring kernel.
+// fused kernel's epilogue or from the scoring kernel, or (small-E kernel) its
+// 32-token histograms.
 static int route_launch(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
                         int E, int k, const moe_route_cfg* cfg, float* logits, int32_t* topk_ids,
                         float* topk_w, int32_t* counts, int32_t* blockcnt, void* ws,
@@ -168,6 +207,12 @@ static int route_launch(const void* x, const void* w, int w_dtype, const float* 
                                      cfg->norm_min, nullptr, topk_ids, topk_w, counts, nullptr,
                                      s),
                     "topk");
+  if (route_is_small(T, H, E, w_dtype))
+    return launched(moe::launch_route_small((const __bf16*)x, (const __bf16*)w, bias, T, E, H, k,
+                                            cfg->scoring, cfg->renormalize, cfg->n_group,
+                                            cfg->topk_group, cfg->route_scale, cfg->norm_min,
+                                            logits, topk_ids, topk_w, counts, blockcnt, s),
+                    "route_small");
   if (route_is_fused(T, H, E, w_dtype, cfg))
     return launched(moe::launch_route_fused((const __bf16*)x, (const __bf16*)w, bias, T, E, H, k,
                                             cfg->scoring, cfg->renormalize, cfg->n_group,
@@ -306,24 +351,27 @@ static int check_permute(const void* x, int x_dtype, const int32_t* topk_ids, in
 
 // The permute's launches over a validated workspace of
 // moe_permute_workspace_bytes(T, E, k) bytes.
-// hist_ready: the workspace already holds the raw block histograms (written
-// by the fused route kernel), so the histogram launch is skipped; T * k > 0.
+// hist (or NULL): raw histograms a route kernel already wrote, so the
+// histogram launch is skipped (T * k > 0): the block histograms [E, nblk] at
+// the workspace's start (hist_tokens = 0) or [E, ceil(T / hist_tokens)]
+// columns of hist_tokens tokens (launch_dispatch_from_hist).
 // stage (fp8 with offsets only, else NULL): fp8_stage_bytes(T, H) bytes for
 // the token-major scales.
 static int permute_launch(const void* x, int x_dtype, const int32_t* topk_ids, int T, int H,
                           int E, int k, int out_dtype, void* xg, float* scales,
                           int32_t* row_token, int32_t* pair_row, int32_t* offsets,
-                          int32_t* counts, void* ws, void* stream, bool hist_ready = false,
-                          void* stage = nullptr) {
+                          int32_t* counts, void* ws, void* stream, int32_t* hist = nullptr,
+                          int hist_tokens = 0, void* stage = nullptr) {
   const bool fp8 = out_dtype == MOE_DTYPE_FP8E4M3FN;
   const int elem = x_dtype == MOE_DTYPE_BF16 ? 2 : 4;
   hipStream_t s = (hipStream_t)stream;
   const int nblk = moe::dispatch_blocks((long long)T * k);
   int32_t* blockcnt = (int32_t*)ws;
   int32_t* totals = (int32_t*)((char*)ws + round256((size_t)E * nblk * 4));
-  int rc = hist_ready
-               ? launched(moe::launch_dispatch_from_hist(topk_ids, T, E, k, blockcnt, totals,
-                                                         row_token, pair_row, offsets, counts, s),
+  int rc = hist
+               ? launched(moe::launch_dispatch_from_hist(topk_ids, T, E, k, hist, hist_tokens,
+                                                         totals, row_token, pair_row, offsets,
+                                                         counts, s),
                           "dispatch_from_hist")
                : launched(moe::launch_dispatch_index(topk_ids, T, E, k, blockcnt, totals,
                                                      row_token, pair_row, offsets, counts, s),
@@ -396,7 +444,7 @@ int moe_permute(const void* x, int x_dtype, const int32_t* topk_ids, int T, int 
       ws_bytes >= moe_permute_fp8_workspace_bytes(T, H, E, k))
     stage = (char*)ws + need;
   return permute_launch(x, x_dtype, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
-                        pair_row, offsets, counts, ws, stream, false, stage);
+                        pair_row, offsets, counts, ws, stream, nullptr, 0, stage);
 }
 
 size_t moe_permute_noalloc_max_scratch_bytes(void) { return kNoallocScratchBytes; }
@@ -422,7 +470,7 @@ int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int
 size_t moe_route_permute_workspace_bytes(int T, int H, int E, int k, int w_dtype) {
   if (T < 0 || H < 0 || E <= 0 || k < 0) return 0;
   return round256(moe_route_workspace_bytes(T, H, E, w_dtype)) +
-         moe_permute_fp8_workspace_bytes(T, H, E, k);
+         moe_permute_fp8_workspace_bytes(T, H, E, k) + route_sub_hist_bytes(T, H, E, k, w_dtype);
 }
 
 int moe_route_permute(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
@@ -447,13 +495,16 @@ int moe_route_permute(const void* x, const void* w, int w_dtype, const float* bi
   // whole permute blocks, it writes the permute's block histograms and the
   // histogram launch is skipped.  The route never writes counts here: the
   // index kernel writes them from the scanned totals.
-  const bool handoff = route_block_hist(T, H, E, k, w_dtype, cfg);
-  rc = route_launch(x, w, w_dtype, bias, T, H, E, k, cfg, logits, topk_ids, topk_w, nullptr,
-                    handoff ? (int32_t*)pws : nullptr, ws, s);
-  if (rc) return rc;
+  const RouteHist handoff = route_block_hist(T, H, E, k, w_dtype, cfg);
   void* stage = (char*)pws + moe_permute_workspace_bytes(T, E, k);
+  int32_t* sub = (int32_t*)((char*)pws + moe_permute_fp8_workspace_bytes(T, H, E, k));
+  int32_t* hist = handoff == kHistSub ? sub : handoff == kHistBlocks ? (int32_t*)pws : nullptr;
+  rc = route_launch(x, w, w_dtype, bias, T, H, E, k, cfg, logits, topk_ids, topk_w, nullptr, hist,
+                    ws, s);
+  if (rc) return rc;
   return permute_launch(x, MOE_DTYPE_BF16, topk_ids, T, H, E, k, out_dtype, xg, scales, row_token,
-                        pair_row, offsets, counts, pws, stream, handoff,
+                        pair_row, offsets, counts, pws, stream, hist,
+                        handoff == kHistSub ? moe::route_small_tokens() : 0,
                         fp8_stage_bytes(T, H) > 0 ? stage : nullptr);
 }
 

@@ -63,6 +63,15 @@ hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bia
                               float route_scale, float norm_min, float* logits, int32_t* ids,
                               float* wout, int32_t* counts, int32_t* blockcnt, void* ws,
                               hipStream_t s);
+// The router GEMM + scoring for few experts (route_small.hip): E = 8 or 16,
+// bf16 weights, H % 1024 == 0.  subcnt (or NULL): the block histograms of its
+// route_small_tokens()-token tiles, [E, ceil(T / route_small_tokens())].
+bool route_small_supported(int E, int H);
+int route_small_tokens();
+hipError_t launch_route_small(const __bf16* x, const __bf16* w, const float* bias, int T, int E,
+                              int H, int k, int scoring, int renorm, int n_group, int topk_group,
+                              float route_scale, float norm_min, float* logits, int32_t* ids,
+                              float* wout, int32_t* counts, int32_t* subcnt, hipStream_t s);
 // K-loop probes of the fused route kernel (E = 256, H = 7168), variants 0-5.
 hipError_t launch_route_probe(int variant, const __bf16* x, const __bf16* w, int T, int H, int E,
                               float* logits, void* ws, hipStream_t s);
@@ -71,10 +80,12 @@ hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_
                                  int32_t* totals, int32_t* row_token, int32_t* pair_row,
                                  int32_t* offsets, int32_t* counts, hipStream_t s);
 // launch_dispatch_index without its histogram launch: blockcnt already holds
-// the raw block histograms [E, dispatch_blocks(T*k)].  T * k > 0.
+// the raw block histograms, [E, dispatch_blocks(T*k)] (sub_tokens = 0) or
+// [E, ceil(T / sub_tokens)] of sub_tokens-token columns.  T * k > 0.
 hipError_t launch_dispatch_from_hist(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
-                                     int32_t* totals, int32_t* row_token, int32_t* pair_row,
-                                     int32_t* offsets, int32_t* counts, hipStream_t s);
+                                     int sub_tokens, int32_t* totals, int32_t* row_token,
+                                     int32_t* pair_row, int32_t* offsets, int32_t* counts,
+                                     hipStream_t s);
 hipError_t launch_gather(const void* x, int elem_bytes, const int32_t* pair_row, int T, int H,
                          int k, void* xg, hipStream_t s);
 // stage (or NULL): T * (H/128) fp32 of workspace for the token-major scales,
@@ -122,5 +133,9 @@ constexpr int kPairsPerBlock = 256;
 inline int dispatch_blocks(long long npairs) {
   return (int)((npairs + kPairsPerBlock - 1) / kPairsPerBlock);
 }
+// Histogram columns up to which every index block sums the raw columns itself
+// (no scan launch): E * ncol <= kDispatchSumMax.
+constexpr long long kDispatchSumMax = 8192;
+inline bool dispatch_sum_path(int E, long long ncol) { return (long long)E * ncol <= kDispatchSumMax; }
 
 }  // namespace moe

@@ -1,0 +1,263 @@
+// Stages 1-2 fused for few experts (E = 8 or 16, bf16 weights): the router
+// GEMM and the scoring in one kernel.
+//
+// Replaces, for the Mixtral-like shapes, the reference's cublasGemmEx router
+// GEMM (K:4327-4339) followed by topk_kernel (K:1829-1920).  With E <= 16 the
+// router GEMM is an x stream: 8 or 16 weight rows (64-128 KB at H = 4096,
+// resident in L2) against every token row.  The two-kernel path needs the K
+// range split over four blocks to fill the chip, and a second kernel to add
+// the partial logits and score them.  Here a 256-thread block owns 32 tokens
+// and its four waves split K instead (a quarter each), so the partial sums
+// meet in LDS and the same block scores its tokens:
+//
+//   K loop   each wave streams its quarter of K through its own LDS ring:
+//            64-wide K steps of the 32 token rows and the E weight rows,
+//            brought in by the gfx950 LDS DMA (8 rows x 128 B per wave
+//            instruction, XOR-swizzled 16-byte chunks), 2 steps in flight,
+//            then two v_mfma_f32_16x16x32_bf16 (one per 16-row half) per
+//            32 k.  Only the wave that loads a ring reads it, so the loop
+//            has no barrier.  The weight fragment's 16 columns hold expert
+//            fr % E (at E = 8 columns 8..15 repeat 0..7 and are dropped).
+//            Measured at C2, slower alternatives: the fragments loaded
+//            straight into registers (16 rows x 64 B per load instruction,
+//            no LDS) 16.5 us; the standalone GEMM's pipeline (two waves per
+//            quarter sharing a ring, one block-wide barrier per step)
+//            15.5 us; 16 weight rows loaded at E = 8 13.2 us; shipped 13.0 us,
+//            against 12.2 + 4.8 us for the two-kernel path's GEMM and scoring.
+//   epilogue the four partial tiles go to LDS (over the rings) as
+//            [token][quarter][expert]; the logits are their sum in quarter
+//            order ((p0 + p1) + p2) + p3 -- the order the scoring kernel adds
+//            the two-kernel path's four K partitions in, with the same K steps
+//            and the same MFMA lane-to-k mapping, so the logits equal that
+//            path's where it splits K in four (C2) -- and G = E/V lanes per
+//            token score them with the scoring kernel's per-token routine
+//            (bit-identical selection on identical logits).  The block's
+//            expert histogram goes to counts and, with subcnt, to column
+//            blockIdx.x of the [E, ceil(T/32)] 32-token histograms the
+//            permute's index kernel sums (no histogram launch).
+#include "moe_common.h"
+#include "score_token.h"
+
+namespace moe {
+
+namespace rs {
+constexpr int TB = 32;  // tokens per block (two 16-row MFMA fragments)
+// K parts (one wave each) and ring stages per wave.  Measured at C2 (T = 8192,
+// H = 4096, E = 8; kernel-trace medians): 4 waves x 3 stages 13.0 us, x 4-6
+// stages 13.1-13.3, 8 waves x 3 stages 14.1, 2 waves x 8-12 stages 19-20.
+constexpr int NG = 4, NS = 3;
+constexpr int BK = 64, ROWB = BK * 2, CH = 8, RPI = 8;  // K step, LDS row bytes, 16-byte chunks
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & (CH - 1); }
+}  // namespace rs
+
+// NG waves, wave g owning K part g (H / NG, whole 64-wide steps) of all 32
+// tokens, each on its own NS-stage LDS ring.
+template <int E, int V, int KK, int SC, int NG, int NS>
+__global__ __launch_bounds__(64 * NG) void route_small_kernel(
+    const __bf16* __restrict__ x, const __bf16* __restrict__ w, const float* __restrict__ bias,
+    int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
+    float norm_min, float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ wout,
+    int* __restrict__ counts, int* __restrict__ subcnt, int nsub) {
+#pragma clang fp contract(off)
+  using namespace rs;
+  constexpr int NT = 64 * NG;
+  static_assert(E == 8 || E == 16, "one 16-column weight fragment");
+  // a stage: TB token rows and the E weight rows, 8 rows x 128 B per DMA instruction
+  constexpr int STAGE_B = (TB + E) * ROWB;
+  constexpr int NQ = (TB + E) / RPI;
+  constexpr int RING_B = NG * NS * STAGE_B;
+  constexpr int PART_B = TB * NG * E * 4;
+  // the partial tiles reuse the rings once every wave has left its K loop
+  __shared__ __attribute__((aligned(1024))) char lds[RING_B > PART_B ? RING_B : PART_B];
+  __shared__ int hist[E];
+  float* const part = reinterpret_cast<float*>(lds);  // [token][K part][expert]
+
+  const int lane = threadIdx.x & 63;
+  const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's K part
+  const long long m0 = (long long)blockIdx.x * TB;
+  const int kw = H / NG;
+  const int KT = kw / BK;
+  char* const wring = lds + g * NS * STAGE_B;
+
+  // Per-lane source of each DMA instruction of a stage: stage rows [0, TB)
+  // are token rows (past T: a copy of row T-1, never stored), rows
+  // [TB, TB + E) the weight rows.
+  const __bf16* src[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int r = q * RPI + lane / CH;  // stage row
+    const int p = lane % CH;
+    const __bf16* base;
+    if (r < TB) {
+      long long t = m0 + r;
+      if (t >= T) t = T - 1;
+      base = x + t * H;
+    } else {
+      base = w + (long long)(r - TB) * H;
+    }
+    src[q] = base + (long long)g * kw + (p ^ swz(r)) * 8;
+  }
+  auto issue = [&](int kt, int st) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      auto* dst = (__attribute__((address_space(3))) void*)(wring + st * STAGE_B + q * 1024);
+      __builtin_amdgcn_global_load_lds((const void*)(src[q] + kt * BK), dst, 16, 0, 0);
+    }
+  };
+
+  f32x4 acc0 = (f32x4){0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < KT) issue(st, st);
+  const int fr = lane & 15, fc = lane >> 4;
+  for (int kt = 0; kt < KT; ++kt) {
+    // Stage kt is in LDS once at most NS-2 later stages are outstanding (only
+    // this wave's DMA loads are in flight here, and only this wave reads its
+    // ring: no barrier).  The slot refilled next held stage kt-1, whose
+    // fragment reads the MFMAs of step kt-1 have consumed.
+    if (kt + NS - 2 < KT)
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"((NS - 2) * NQ) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (kt + NS - 1 < KT) issue(kt + NS - 1, (kt + NS - 1) % NS);
+    const char* sb = wring + (kt % NS) * STAGE_B;
+#pragma unroll
+    for (int kk = 0; kk < BK / 32; ++kk) {
+      // lane (fr, fc) feeds k = kk*32 + fc*8 .. +8 of row fr: the standalone
+      // GEMM's mapping, so the parts' sums are its K partitions' bit for bit
+      const int c = kk * 4 + fc;
+      // the weight fragment's 16 columns: expert fr % E (at E = 8 columns
+      // 8..15 repeat 0..7 and are dropped)
+      const int rb = TB + fr % E, r1 = 16 + fr;
+      const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(sb + fr * ROWB + ((c ^ swz(fr)) * 16));
+      const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(sb + r1 * ROWB + ((c ^ swz(r1)) * 16));
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(sb + rb * ROWB + ((c ^ swz(rb)) * 16));
+      acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, acc1, 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every ring is read: the partial tiles may overwrite them
+
+  // ---- partial tiles to LDS: lane (fr, fc) holds column fr, rows fc*4 .. fc*4+3
+  // of each 16-row half
+  if (fr < E) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      part[((fc * 4 + i) * NG + g) * E + fr] = acc0[i];
+      part[((16 + fc * 4 + i) * NG + g) * E + fr] = acc1[i];
+    }
+  }
+  const bool hists = counts || subcnt;
+  if (threadIdx.x < E) hist[threadIdx.x] = 0;
+  __syncthreads();
+
+  // ---- scoring: G = E/V lanes per token
+  constexpr int G = E / V;
+  constexpr int TPP = NT / G;  // tokens per pass
+  static_assert(TB % TPP == 0 || TPP % TB == 0, "token passes");
+  const int gl = threadIdx.x % G;
+  const int e0 = gl * V;
+  float bl[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) bl[j] = bias ? bias[e0 + j] : 0.0f;
+  const int k = KK > 0 ? KK : k_rt;
+  for (int tl = threadIdx.x / G; tl < TB; tl += TPP) {
+    const long long t = m0 + tl;
+    const float* row = part + tl * NG * E;
+    float l[1][V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      float v = row[e0 + j];
+#pragma unroll
+      for (int p = 1; p < NG; ++p) v = v + row[p * E + e0 + j];
+      l[0][j] = v;
+    }
+    const bool valid[1] = {t < T};
+    if (valid[0]) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) logits[t * E + e0 + j] = l[0][j];
+    }
+    const float* const rows[1] = {row};
+    int my_id[1];
+    float wv[1];
+    score_tokens<E, V, KK, SC, 1>(l, bl, rows, NG, valid, gl, k_rt, renorm, n_group, topk_group,
+                                  route_scale, norm_min, my_id, wv);
+    if (valid[0] && gl < k) {
+      ids[t * k + gl] = my_id[0];
+      wout[t * k + gl] = wv[0];
+      if (hists) atomicAdd(&hist[my_id[0]], 1);
+    }
+  }
+  if (hists) {
+    __syncthreads();
+    if (threadIdx.x < E) {
+      const int c = hist[threadIdx.x];
+      if (counts && c) atomicAdd(counts + threadIdx.x, c);
+      if (subcnt) subcnt[(long long)threadIdx.x * nsub + blockIdx.x] = c;
+    }
+  }
+}
+
+__global__ void rs_zero_kernel(int* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// E = 8 or 16 and H a multiple of 256 (four parts of whole 64-wide K steps).
+bool route_small_supported(int E, int H) {
+  return (E == 8 || E == 16) && H > 0 && H % (rs::NG * rs::BK) == 0;
+}
+
+int route_small_tokens() { return rs::TB; }
+
+template <int E, int V, int KK, int SC>
+static hipError_t launch_rs(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
+                            int k, int renorm, int n_group, int topk_group, float route_scale,
+                            float norm_min, float* logits, int32_t* ids, float* wout,
+                            int32_t* counts, int32_t* subcnt, hipStream_t s) {
+  const int nsub = (T + rs::TB - 1) / rs::TB;
+  hipLaunchKernelGGL((route_small_kernel<E, V, KK, SC, rs::NG, rs::NS>), dim3((unsigned)nsub),
+                     dim3(64 * rs::NG), 0, s, x, w, bias, T, H, k, renorm, n_group, topk_group,
+                     route_scale, norm_min, logits, ids, wout, counts, subcnt, nsub);
+  return hipGetLastError();
+}
+
+template <int E, int V>
+static hipError_t launch_rs_cfg(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
+                                int k, int scoring, int renorm, int n_group, int topk_group,
+                                float route_scale, float norm_min, float* logits, int32_t* ids,
+                                float* wout, int32_t* counts, int32_t* subcnt, hipStream_t s) {
+#define MOE_RS_ARGS x, w, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, \
+                    logits, ids, wout, counts, subcnt, s
+#define MOE_RS_K(SC)                                           \
+  return k == 2 ? launch_rs<E, V, 2, SC>(MOE_RS_ARGS)          \
+                : launch_rs<E, V, 0, SC>(MOE_RS_ARGS);
+  if (scoring == kScoreSoftmax) MOE_RS_K(kScoreSoftmax)
+  if (scoring == kScoreSigmoidGroup) MOE_RS_K(kScoreSigmoidGroup)
+  MOE_RS_K(kScoreSoftmaxBias)
+#undef MOE_RS_K
+#undef MOE_RS_ARGS
+}
+
+hipError_t launch_route_small(const __bf16* x, const __bf16* w, const float* bias, int T, int E,
+                              int H, int k, int scoring, int renorm, int n_group, int topk_group,
+                              float route_scale, float norm_min, float* logits, int32_t* ids,
+                              float* wout, int32_t* counts, int32_t* subcnt, hipStream_t s) {
+  if (counts) {
+    hipLaunchKernelGGL(rs_zero_kernel, dim3(1), dim3(64), 0, s, counts, E);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (T == 0) return hipSuccess;
+  // lanes of min(2, E/8) experts: a sigmoid group holds at least two
+  const int V = topk_lane_width(E, scoring, n_group);
+  if (E == 8 && V == 1)
+    return launch_rs_cfg<8, 1>(x, w, bias, T, H, k, scoring, renorm, n_group, topk_group,
+                               route_scale, norm_min, logits, ids, wout, counts, subcnt, s);
+  if (E == 16 && V == 2)
+    return launch_rs_cfg<16, 2>(x, w, bias, T, H, k, scoring, renorm, n_group, topk_group,
+                                route_scale, norm_min, logits, ids, wout, counts, subcnt, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace moe

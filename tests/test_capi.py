@@ -116,8 +116,15 @@ def _router_ksplit(T, H, N):
     return ks
 
 
+def _route_small(H, E, fp32):
+    """The small-E GEMM + scoring kernel: E = 8 or 16, bf16 weights, H % 256 == 0."""
+    return not fp32 and E in (8, 16) and H > 0 and H % 256 == 0
+
+
 def _route_ws(T, H, E, fp32):
     r256 = lambda b: (b + 255) // 256 * 256
+    if _route_small(H, E, fp32):
+        return 0  # no K partitions: the four waves of a block split K and add in LDS
     N = 2 * E if fp32 else E
     parts = (N // E) * _router_ksplit(T, H, N)
     b = r256(2 * E * H * 2) if fp32 else 0
@@ -142,7 +149,11 @@ def test_workspace_sizes():
     assert L.moe_route_workspace_bytes(32768, 7168, 256, 1) == 2 * 256 * 7168 * 2 + 32768 * 512 * 4
     assert L.moe_route_workspace_bytes(65536, 7168, 256, 0) == 256 * 7168 * 2
     assert L.moe_route_workspace_bytes(32768, 4096, 256, 0) == 0   # no fused kernel, no K split
+    # C2 (Mixtral) shape: the small-E kernel, no workspace; fp32 weights still split hi/lo
+    assert L.moe_route_workspace_bytes(8192, 4096, 8, 0) == 0
+    assert L.moe_route_workspace_bytes(8192, 4096, 8, 1) > 0
     for T, H, E in [(1, 64, 8), (100, 128, 8), (512, 1024, 8), (8192, 4096, 8), (16384, 2048, 128),
+                    (300, 2048, 16), (300, 1536, 16),
                     (1571, 8192, 64), (32768, 7168, 256), (300, 7168, 256), (4096, 8192, 64)]:
         for fp32 in (0, 1):
             assert L.moe_route_workspace_bytes(T, H, E, fp32) == _route_ws(T, H, E, fp32), (T, H, E, fp32)
@@ -382,13 +393,23 @@ def test_route_permute_workspace_and_validation():
     L = M.lib()
     r256 = lambda n: (n + 255) // 256 * 256
     for (T, H, E, k) in [(32768, 7168, 256, 8), (16384, 2048, 128, 8), (100, 128, 8, 2),
-                         (0, 7168, 256, 8), (4133, 7168, 256, 5), (100, 64, 8, 2)]:
+                         (0, 7168, 256, 8), (4133, 7168, 256, 5), (100, 64, 8, 2),
+                         (8192, 4096, 8, 2), (1001, 1024, 8, 2), (300, 2048, 16, 8),
+                         (300, 2048, 16, 3), (70000, 4096, 8, 2), (5000, 4096, 16, 1)]:
         stage = r256(T * (H // 128) * 4) if T > 0 and H % 128 == 0 else 0
+        # the small-E route's 32-token histograms [E, ceil(T/32)] for the permute, when
+        # 256 / k tokens are whole 32-token columns and E * columns <= 8192
+        ncol = -(-T // 32)
+        sub = r256(E * ncol * 4) if (T > 0 and _route_small(H, E, 0) and 256 % k == 0
+                                     and (256 // k) % 32 == 0 and E * ncol <= 8192) else 0
         assert L.moe_permute_fp8_workspace_bytes(T, H, E, k) == \
             L.moe_permute_workspace_bytes(T, E, k) + stage
         assert L.moe_route_permute_workspace_bytes(T, H, E, k, 0) == \
             r256(L.moe_route_workspace_bytes(T, H, E, 0)) + L.moe_permute_workspace_bytes(T, E, k) \
-            + stage
+            + stage + sub, (T, H, E, k)
+    # C2: 8 x 256 columns of 32 tokens
+    assert L.moe_route_permute_workspace_bytes(8192, 4096, 8, 2, 0) == \
+        L.moe_permute_fp8_workspace_bytes(8192, 4096, 8, 2) + 8 * 256 * 4
     assert L.moe_permute_fp8_workspace_bytes(32768, 7168, 256, 8) - \
         L.moe_permute_workspace_bytes(32768, 256, 8) == 32768 * 56 * 4
     assert L.moe_route_permute_workspace_bytes(-1, 7168, 256, 8, 0) == 0

@@ -7,7 +7,9 @@ Where the route is the fused kernel and k divides 256 with 256 / k tokens
 fitting its token tile (E = 256: k in {2, 4, 8}; E = 128: k in {4, 8}), the
 fused kernel's epilogue writes the permute's block histograms; on the
 two-kernel route (other shapes, fp32 weights) the scoring kernel writes them
-when k divides 256.  These cases check both handoffs: token counts that end
+when k divides 256; the small-E route kernel (E = 8 or 16, H % 256 == 0)
+writes one histogram per 32 tokens, which the index kernel sums per block
+when 256 / k is a multiple of 32 and E x columns <= 8192.  These cases check both handoffs: token counts that end
 inside a block of 256 pairs and inside a route tile (1, 33, 129, 1000,
 4133), k = 5, 3 and (fused) 1 (no handoff), unfused shapes from E = 8 to
 E = 256, C2's split-K GEMM and fp32 weights (the hi/lo split route of the
@@ -119,14 +121,21 @@ CASES = [
     (128, 2048, 2, 200, False, False),     # no handoff: 128-token blocks > tile
     (64, 1024, 8, 1000, False, False),     # unfused route: the scoring kernel's handoff
     (64, 8192, 8, 1571, False, True),      # fp32 weights (hi/lo split): the run() shape
-    (8, 4096, 2, 8192, False, False),      # C2's shape: split-K GEMM, 128-token blocks
+    (8, 4096, 2, 8192, False, False),      # C2's shape: the small-E route, 4 columns per block
+    (8, 3968, 2, 8192, False, False),      # H % 256 != 0: split-K GEMM + scoring kernel
     (8, 1024, 2, 1001, True, False),       # a last block of 18 pairs
-    (16, 512, 1, 300, False, False),       # 256-token blocks, 8 scoring passes
+    (16, 448, 1, 300, False, False),       # scoring kernel: 256-token blocks, 8 passes
     (32, 512, 4, 97, False, False),
     (128, 1024, 8, 333, False, False),     # unfused at E = 128
     (256, 1024, 8, 555, False, False),     # unfused at E = 256 (sigmoid groups, 16-token passes)
     (256, 1024, 2, 257, True, False),
     (64, 1024, 3, 400, False, False),      # no handoff: 256 % 3 != 0
+    # the small-E route (E = 8 / 16, H % 256 == 0): 32-token histogram columns
+    (16, 2048, 8, 333, False, False),      # one column per permute block
+    (16, 1024, 4, 1000, True, False),      # two columns per block
+    (8, 2048, 1, 777, False, False),       # eight columns per block
+    (8, 4096, 3, 500, False, False),       # no handoff: 256 % 3 != 0
+    (16, 2048, 2, 20000, False, True),     # no handoff: 16 x 625 columns > 8192
 ]
 
 
