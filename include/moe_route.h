@@ -82,6 +82,9 @@ const char* moe_last_error_string(void);
  *   - E = 256, H = 7168 or E = 128, H = 2048 with bf16 weights: the router
  *     GEMM and the scoring run as one kernel that reads a fragment-major copy
  *     of the weight, E*H*2 bytes (3.5 MiB / 512 KiB), rewritten by every call.
+ * E = 8 or 16 with bf16 weights and H % 256 == 0 (the Mixtral shape): zero;
+ * one kernel does the GEMM, with K split across the four waves of a block,
+ * and the scoring.
  * The size does not depend on cfg; it covers whichever path the call takes. */
 size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype);
 
@@ -177,11 +180,16 @@ int moe_permute_noalloc(const void* x, int x_dtype, const int32_t* topk_ids, int
  * E = 256, {4, 8} at E = 128), else the scoring kernel when 256 / k is a
  * multiple of the tokens one of its passes scores (k in {1, 2, 4, 8}: 32
  * tokens per pass at E <= 128, 16 at E = 256, fewer with expert groups
- * narrower than 16); otherwise the
- * two stages run as moe_route and moe_permute would.  counts: the permute's.
+ * narrower than 16).  The small-E route kernel (E = 8 or 16, see
+ * moe_route) writes one histogram per 32 tokens instead, which the index
+ * kernel sums per permute block, when 256 / k is a multiple of 32 (k in
+ * {1, 2, 4, 8}) and E * ceil(T / 32) <= 8192.  Otherwise the two stages run
+ * as moe_route and moe_permute would.  counts: the permute's.
  * ws: moe_route_permute_workspace_bytes(T, H, E, k, w_dtype) bytes, 16-byte
  * aligned (the route's workspace, rounded up to 256 bytes, then the
- * permute's with its fp8 scale stage, moe_permute_fp8_workspace_bytes).
+ * permute's with its fp8 scale stage, moe_permute_fp8_workspace_bytes, then,
+ * for the small-E kernel's handoff, E * ceil(T / 32) int32 rounded up to 256
+ * bytes).
  * Every argument of both stages is checked before any launch. */
 size_t moe_route_permute_workspace_bytes(int T, int H, int E, int k, int w_dtype);
 int moe_route_permute(const void* x, const void* w, int w_dtype, const float* bias, int T, int H,
