@@ -87,6 +87,33 @@ __device__ __forceinline__ unsigned int cvt_fp8x4(float a, float b, float c, flo
 // scattered 32-byte runs per token cost more than the fp8 rows they describe
 // (C5: gather 438 against 403 us and the combine after it 762 against 732 us
 // with and without them).
+// One 16-element chunk c of x: its e4m3fn bytes and its 1x128 block's scale.
+// The 8 lanes of a block (consecutive, 8-aligned) must all call it.
+__device__ __forceinline__ void quant_chunk(const u32x4* __restrict__ x, long long c,
+                                            u32x4& packed, float& scale) {
+  const u32x4 r0 = x[2 * c], r1 = x[2 * c + 1];
+  float f[16];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f[2 * q] = bf16lo(r0[q]);
+    f[2 * q + 1] = bf16hi(r0[q]);
+    f[8 + 2 * q] = bf16lo(r1[q]);
+    f[8 + 2 * q + 1] = bf16hi(r1[q]);
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) amax = fmaxf(amax, fabsf(f[q]));
+#pragma unroll
+  for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  scale = __fdiv_rn(fmaxf(amax, 1e-10f), 448.0f);
+  float qv[16];
+#pragma unroll
+  for (int q = 0; q < 16; ++q) qv[q] = fminf(fmaxf(__fdiv_rn(f[q], scale), -448.0f), 448.0f);
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    packed[q] = cvt_fp8x4(qv[4 * q], qv[4 * q + 1], qv[4 * q + 2], qv[4 * q + 3]);
+}
+
 __global__ __launch_bounds__(256) void gather_fp8_kernel(const u32x4* __restrict__ x,
                                                          const int* __restrict__ pair_row,
                                                          long long nchunks, int cpr, int nb,
@@ -100,28 +127,9 @@ __global__ __launch_bounds__(256) void gather_fp8_kernel(const u32x4* __restrict
        c += (long long)gridDim.x * 256) {
     const int t = (int)(c / cpr);
     const int v = (int)(c - (long long)t * cpr);
-    const u32x4 r0 = x[2 * c], r1 = x[2 * c + 1];
-    float f[16];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      f[2 * q] = bf16lo(r0[q]);
-      f[2 * q + 1] = bf16hi(r0[q]);
-      f[8 + 2 * q] = bf16lo(r1[q]);
-      f[8 + 2 * q + 1] = bf16hi(r1[q]);
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) amax = fmaxf(amax, fabsf(f[q]));
-#pragma unroll
-    for (int o = 1; o < 8; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    const float scale = __fdiv_rn(fmaxf(amax, 1e-10f), 448.0f);
-    float qv[16];
-#pragma unroll
-    for (int q = 0; q < 16; ++q) qv[q] = fminf(fmaxf(__fdiv_rn(f[q], scale), -448.0f), 448.0f);
     u32x4 packed;
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      packed[q] = cvt_fp8x4(qv[4 * q], qv[4 * q + 1], qv[4 * q + 2], qv[4 * q + 3]);
+    float scale;
+    quant_chunk(x, c, packed, scale);
     const int* pr = pair_row + (long long)t * k;
     const int blk = v >> 3;
     if (stage && lane8 == 0) stage[(long long)t * nb + blk] = scale;
