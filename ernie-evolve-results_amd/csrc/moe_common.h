@@ -63,15 +63,18 @@ hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bia
                               float route_scale, float norm_min, float* logits, int32_t* ids,
                               float* wout, int32_t* counts, int32_t* blockcnt, void* ws,
                               hipStream_t s);
-// The router GEMM + scoring for few experts (route_small.hip): E = 8 or 16,
-// bf16 weights, H % 1024 == 0.  subcnt (or NULL): the block histograms of its
-// route_small_tokens()-token tiles, [E, ceil(T / route_small_tokens())].
-bool route_small_supported(int E, int H);
+// The router GEMM + scoring for few experts (route_small.hip): E = 8 or 16
+// with bf16 weights, or E = 8 with split = true (w is an fp32 weight's hi/lo
+// bf16 split [2E, H], launch_wsplit's); H % 256 == 0.  subcnt (or NULL): the
+// block histograms of its route_small_tokens()-token tiles,
+// [E, ceil(T / route_small_tokens())].
+bool route_small_supported(int E, int H, bool split);
 int route_small_tokens();
-hipError_t launch_route_small(const __bf16* x, const __bf16* w, const float* bias, int T, int E,
-                              int H, int k, int scoring, int renorm, int n_group, int topk_group,
-                              float route_scale, float norm_min, float* logits, int32_t* ids,
-                              float* wout, int32_t* counts, int32_t* subcnt, hipStream_t s);
+hipError_t launch_route_small(const __bf16* x, const __bf16* w, bool split, const float* bias,
+                              int T, int E, int H, int k, int scoring, int renorm, int n_group,
+                              int topk_group, float route_scale, float norm_min, float* logits,
+                              int32_t* ids, float* wout, int32_t* counts, int32_t* subcnt,
+                              hipStream_t s);
 // K-loop probes of the fused route kernel (E = 256, H = 7168), variants 0-5.
 hipError_t launch_route_probe(int variant, const __bf16* x, const __bf16* w, int T, int H, int E,
                               float* logits, void* ws, hipStream_t s);

@@ -51,8 +51,10 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & (CH - 1); }
 }  // namespace rs
 
 // NG waves, wave g owning K part g (H / NG, whole 64-wide steps) of all 32
-// tokens, each on its own NS-stage LDS ring.
-template <int E, int V, int KK, int SC, int NG, int NS>
+// tokens, each on its own NS-stage LDS ring.  HL = 2: w is an fp32 weight's
+// hi/lo bf16 split [2E, H] (E = 8: the 16 columns are the 8 hi then the 8 lo
+// rows), and a logit is the sum of 2 * NG partials, hi then lo per K part.
+template <int E, int V, int KK, int SC, int NG, int NS, int HL>
 __global__ __launch_bounds__(64 * NG) void route_small_kernel(
     const __bf16* __restrict__ x, const __bf16* __restrict__ w, const float* __restrict__ bias,
     int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
@@ -61,16 +63,19 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
 #pragma clang fp contract(off)
   using namespace rs;
   constexpr int NT = 64 * NG;
-  static_assert(E == 8 || E == 16, "one 16-column weight fragment");
-  // a stage: TB token rows and the E weight rows, 8 rows x 128 B per DMA instruction
-  constexpr int STAGE_B = (TB + E) * ROWB;
-  constexpr int NQ = (TB + E) / RPI;
+  static_assert((E == 8 || E == 16) && (HL == 1 || HL == 2) && HL * E <= 16,
+                "one 16-column weight fragment");
+  constexpr int NW = HL * E;    // weight rows
+  constexpr int NP = NG * HL;   // partial logit blocks per token
+  // a stage: TB token rows and the NW weight rows, 8 rows x 128 B per DMA instruction
+  constexpr int STAGE_B = (TB + NW) * ROWB;
+  constexpr int NQ = (TB + NW) / RPI;
   constexpr int RING_B = NG * NS * STAGE_B;
-  constexpr int PART_B = TB * NG * E * 4;
+  constexpr int PART_B = TB * NP * E * 4;
   // the partial tiles reuse the rings once every wave has left its K loop
   __shared__ __attribute__((aligned(1024))) char lds[RING_B > PART_B ? RING_B : PART_B];
   __shared__ int hist[E];
-  float* const part = reinterpret_cast<float*>(lds);  // [token][K part][expert]
+  float* const part = reinterpret_cast<float*>(lds);  // [token][K part][half][expert]
 
   const int lane = threadIdx.x & 63;
   const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // this wave's K part
@@ -81,7 +86,7 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
 
   // Per-lane source of each DMA instruction of a stage: stage rows [0, TB)
   // are token rows (past T: a copy of row T-1, never stored), rows
-  // [TB, TB + E) the weight rows.
+  // [TB, TB + NW) the weight rows.
   const __bf16* src[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
@@ -126,9 +131,9 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
       // lane (fr, fc) feeds k = kk*32 + fc*8 .. +8 of row fr: the standalone
       // GEMM's mapping, so the parts' sums are its K partitions' bit for bit
       const int c = kk * 4 + fc;
-      // the weight fragment's 16 columns: expert fr % E (at E = 8 columns
-      // 8..15 repeat 0..7 and are dropped)
-      const int rb = TB + fr % E, r1 = 16 + fr;
+      // the weight fragment's 16 columns: weight row fr % NW (at E = 8 with
+      // one half, columns 8..15 repeat 0..7 and are dropped)
+      const int rb = TB + fr % NW, r1 = 16 + fr;
       const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(sb + fr * ROWB + ((c ^ swz(fr)) * 16));
       const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(sb + r1 * ROWB + ((c ^ swz(r1)) * 16));
       const bf16x8 b = *reinterpret_cast<const bf16x8*>(sb + rb * ROWB + ((c ^ swz(rb)) * 16));
@@ -140,11 +145,12 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
 
   // ---- partial tiles to LDS: lane (fr, fc) holds column fr, rows fc*4 .. fc*4+3
   // of each 16-row half
-  if (fr < E) {
+  // column fr = half h, expert e; the partial block index is g * HL + h
+  if (fr < NW) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      part[((fc * 4 + i) * NG + g) * E + fr] = acc0[i];
-      part[((16 + fc * 4 + i) * NG + g) * E + fr] = acc1[i];
+      part[((fc * 4 + i) * NG + g) * NW + fr] = acc0[i];
+      part[((16 + fc * 4 + i) * NG + g) * NW + fr] = acc1[i];
     }
   }
   const bool hists = counts || subcnt;
@@ -163,13 +169,13 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
   const int k = KK > 0 ? KK : k_rt;
   for (int tl = threadIdx.x / G; tl < TB; tl += TPP) {
     const long long t = m0 + tl;
-    const float* row = part + tl * NG * E;
+    const float* row = part + tl * NP * E;
     float l[1][V];
 #pragma unroll
     for (int j = 0; j < V; ++j) {
       float v = row[e0 + j];
 #pragma unroll
-      for (int p = 1; p < NG; ++p) v = v + row[p * E + e0 + j];
+      for (int p = 1; p < NP; ++p) v = v + row[p * E + e0 + j];
       l[0][j] = v;
     }
     const bool valid[1] = {t < T};
@@ -180,7 +186,7 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
     const float* const rows[1] = {row};
     int my_id[1];
     float wv[1];
-    score_tokens<E, V, KK, SC, 1>(l, bl, rows, NG, valid, gl, k_rt, renorm, n_group, topk_group,
+    score_tokens<E, V, KK, SC, 1>(l, bl, rows, NP, valid, gl, k_rt, renorm, n_group, topk_group,
                                   route_scale, norm_min, my_id, wv);
     if (valid[0] && gl < k) {
       ids[t * k + gl] = my_id[0];
@@ -203,26 +209,27 @@ __global__ void rs_zero_kernel(int* __restrict__ p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// E = 8 or 16 and H a multiple of 256 (four parts of whole 64-wide K steps).
-bool route_small_supported(int E, int H) {
-  return (E == 8 || E == 16) && H > 0 && H % (rs::NG * rs::BK) == 0;
+// H a multiple of 256 (four parts of whole 64-wide K steps); E = 8 or 16 with
+// bf16 weights, E = 8 with an fp32 weight's hi/lo split (16 weight rows).
+bool route_small_supported(int E, int H, bool split) {
+  return (split ? E == 8 : (E == 8 || E == 16)) && H > 0 && H % (rs::NG * rs::BK) == 0;
 }
 
 int route_small_tokens() { return rs::TB; }
 
-template <int E, int V, int KK, int SC>
+template <int E, int V, int KK, int SC, int HL>
 static hipError_t launch_rs(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
                             int k, int renorm, int n_group, int topk_group, float route_scale,
                             float norm_min, float* logits, int32_t* ids, float* wout,
                             int32_t* counts, int32_t* subcnt, hipStream_t s) {
   const int nsub = (T + rs::TB - 1) / rs::TB;
-  hipLaunchKernelGGL((route_small_kernel<E, V, KK, SC, rs::NG, rs::NS>), dim3((unsigned)nsub),
+  hipLaunchKernelGGL((route_small_kernel<E, V, KK, SC, rs::NG, rs::NS, HL>), dim3((unsigned)nsub),
                      dim3(64 * rs::NG), 0, s, x, w, bias, T, H, k, renorm, n_group, topk_group,
                      route_scale, norm_min, logits, ids, wout, counts, subcnt, nsub);
   return hipGetLastError();
 }
 
-template <int E, int V>
+template <int E, int V, int HL>
 static hipError_t launch_rs_cfg(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
                                 int k, int scoring, int renorm, int n_group, int topk_group,
                                 float route_scale, float norm_min, float* logits, int32_t* ids,
@@ -230,8 +237,8 @@ static hipError_t launch_rs_cfg(const __bf16* x, const __bf16* w, const float* b
 #define MOE_RS_ARGS x, w, bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, \
                     logits, ids, wout, counts, subcnt, s
 #define MOE_RS_K(SC)                                           \
-  return k == 2 ? launch_rs<E, V, 2, SC>(MOE_RS_ARGS)          \
-                : launch_rs<E, V, 0, SC>(MOE_RS_ARGS);
+  return k == 2 ? launch_rs<E, V, 2, SC, HL>(MOE_RS_ARGS)      \
+                : launch_rs<E, V, 0, SC, HL>(MOE_RS_ARGS);
   if (scoring == kScoreSoftmax) MOE_RS_K(kScoreSoftmax)
   if (scoring == kScoreSigmoidGroup) MOE_RS_K(kScoreSigmoidGroup)
   MOE_RS_K(kScoreSoftmaxBias)
@@ -239,10 +246,11 @@ static hipError_t launch_rs_cfg(const __bf16* x, const __bf16* w, const float* b
 #undef MOE_RS_ARGS
 }
 
-hipError_t launch_route_small(const __bf16* x, const __bf16* w, const float* bias, int T, int E,
-                              int H, int k, int scoring, int renorm, int n_group, int topk_group,
-                              float route_scale, float norm_min, float* logits, int32_t* ids,
-                              float* wout, int32_t* counts, int32_t* subcnt, hipStream_t s) {
+hipError_t launch_route_small(const __bf16* x, const __bf16* w, bool split, const float* bias,
+                              int T, int E, int H, int k, int scoring, int renorm, int n_group,
+                              int topk_group, float route_scale, float norm_min, float* logits,
+                              int32_t* ids, float* wout, int32_t* counts, int32_t* subcnt,
+                              hipStream_t s) {
   if (counts) {
     hipLaunchKernelGGL(rs_zero_kernel, dim3(1), dim3(64), 0, s, counts, E);
     const hipError_t e = hipGetLastError();
@@ -251,11 +259,17 @@ hipError_t launch_route_small(const __bf16* x, const __bf16* w, const float* bia
   if (T == 0) return hipSuccess;
   // lanes of min(2, E/8) experts: a sigmoid group holds at least two
   const int V = topk_lane_width(E, scoring, n_group);
+  if (split) {
+    if (E == 8 && V == 1)
+      return launch_rs_cfg<8, 1, 2>(x, w, bias, T, H, k, scoring, renorm, n_group, topk_group,
+                                    route_scale, norm_min, logits, ids, wout, counts, subcnt, s);
+    return hipErrorInvalidValue;
+  }
   if (E == 8 && V == 1)
-    return launch_rs_cfg<8, 1>(x, w, bias, T, H, k, scoring, renorm, n_group, topk_group,
+    return launch_rs_cfg<8, 1, 1>(x, w, bias, T, H, k, scoring, renorm, n_group, topk_group,
                                route_scale, norm_min, logits, ids, wout, counts, subcnt, s);
   if (E == 16 && V == 2)
-    return launch_rs_cfg<16, 2>(x, w, bias, T, H, k, scoring, renorm, n_group, topk_group,
+    return launch_rs_cfg<16, 2, 1>(x, w, bias, T, H, k, scoring, renorm, n_group, topk_group,
                                 route_scale, norm_min, logits, ids, wout, counts, subcnt, s);
   return hipErrorInvalidValue;
 }

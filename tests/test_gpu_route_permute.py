@@ -136,6 +136,7 @@ CASES = [
     (8, 2048, 1, 777, False, False),       # eight columns per block
     (8, 4096, 3, 500, False, False),       # no handoff: 256 % 3 != 0
     (16, 2048, 2, 20000, False, True),     # no handoff: 16 x 625 columns > 8192
+    (8, 1024, 2, 512, False, False),       # C1's shape (fp32 weights: the small-E hi/lo route)
 ]
 
 
@@ -146,7 +147,7 @@ def test_route_permute_matches_two_calls(cuda, E, H, k, T, fp8, index_only):
     g = torch.Generator().manual_seed(E + k * 7 + T)
     x = torch.randn(T, H, generator=g).bfloat16().to(cuda)
     w = torch.randn(E, H, generator=g) * 0.02
-    w = (w if H == 8192 else w.bfloat16()).to(cuda)
+    w = (w if H == 8192 or (E, H, T) == (8, 1024, 512) else w.bfloat16()).to(cuda)
     bias = (torch.randn(E, generator=g) * 0.1).to(cuda)
     cfg = cfg_for(E)
     ref = run_pair(x, w, bias, k, cfg, fp8, index_only)

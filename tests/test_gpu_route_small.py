@@ -117,3 +117,48 @@ def test_route_small_repeat(cuda):
     torch.cuda.synchronize()
     for u, v in zip(a, b):
         assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("H,T,k", [(1024, 512, 2), (1024, 1, 2), (4096, 1000, 3), (2048, 33, 1)])
+def test_route_small_fp32_weights(cuda, H, T, k):
+    """E = 8 with an fp32 weight (C1's toy route): the kernel runs on the hi/lo
+    bf16 split (hi = bf16(w), lo = bf16(w - hi)) as 16 weight rows, and each
+    logit is the sum of eight partials, hi then lo per K quarter -- equal, bit
+    for bit, to the standalone GEMM over each quarter of each half added in
+    that order; selection equals the scoring kernel's and the oracle's."""
+    print("route_small fp32 H=%d T=%d k=%d" % (H, T, k), flush=True)
+    E = 8
+    cfg = CFGS["softmax"]
+    L = M.lib()
+    assert L.moe_route_workspace_bytes(T, H, E, 1) == 2 * E * H * 2
+    g = torch.Generator().manual_seed(H + T + k)
+    x = torch.randn(T, H, generator=g).bfloat16().to(cuda)
+    w = (torch.randn(E, H, generator=g) * 0.02).to(cuda)
+    lf, idf, wf, cf = M.route(x, w, None, k, cfg)
+    hi = w.bfloat16()
+    lo = (w - hi.float()).bfloat16()
+    kw = H // 4
+    acc = None
+    for q in range(4):
+        xq = x[:, q * kw:(q + 1) * kw].contiguous()
+        for half in (hi, lo):
+            wq = half[:, q * kw:(q + 1) * kw].contiguous()
+            p = torch.empty(T, E, dtype=torch.float32, device=cuda)
+            rc = L.moe_router_gemm(M._ptr(xq), M._ptr(wq), T, kw, E, M._ptr(p), M._stream(x))
+            assert rc == 0, L.moe_last_error_string()
+            acc = p if acc is None else acc + p
+    ido, wo, co = M.topk(lf, None, k, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(lf, acc), "logits differ from the hi/lo K-quarter GEMMs added in order"
+    assert torch.equal(idf, ido) and torch.equal(wf, wo) and torch.equal(cf, co)
+    ocfg = O.RouteCfg(cfg.scoring, cfg.renormalize, cfg.n_group, cfg.topk_group,
+                      cfg.route_scale, cfg.norm_min)
+    oi, _ = O.score_topk(lf.cpu().numpy(), None, k, ocfg)
+    assert np.array_equal(idf.cpu().numpy(), oi)
+    # the split reconstructs the fp32 weight to 2^-16 relative: the logits sit within
+    # the fp32 summation bound plus that residual of the float64 product with w
+    xd, wd = x.double().cpu(), w.double().cpu()
+    ref = (xd @ wd.t()).numpy()
+    mag = (xd.abs() @ wd.abs().t()).numpy()
+    bound = 2 * H * 2.0 ** -24 * mag + 2.0 ** -16 * mag + 1e-30
+    assert np.all(np.abs(lf.cpu().numpy().astype(np.float64) - ref) <= bound)
