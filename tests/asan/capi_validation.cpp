@@ -60,6 +60,13 @@ int main() {
   // fp32 weights: [2E,H] bf16 hi/lo split + [T,2E] fp32 hi/lo partial logits
   if (moe_route_workspace_bytes(32768, 7168, 256, MOE_DTYPE_FP32) != (size_t)2 * 256 * 7168 * 2 + (size_t)32768 * 512 * 4) ++failures;
   if (moe_permute_workspace_bytes(32768, 256, 8) != (size_t)256 * 1024 * 4 + 1024) ++failures;
+  // C2 (E = 8, bf16): the small-E GEMM + scoring kernel needs no route workspace; through
+  // moe_route_permute it adds its 32-token histograms, 8 experts x 256 columns of int32
+  if (moe_route_workspace_bytes(8192, 4096, 8, MOE_DTYPE_BF16) != 0) ++failures;
+  if (moe_route_workspace_bytes(8192, 4096, 8, MOE_DTYPE_FP32) != (size_t)2 * 8 * 4096 * 2) ++failures;
+  if (moe_route_permute_workspace_bytes(8192, 4096, 8, 2, MOE_DTYPE_BF16) !=
+      moe_permute_fp8_workspace_bytes(8192, 4096, 8, 2) + (size_t)8 * 256 * 4)
+    ++failures;
   // route + permute in one call: the workspace and both stages' checks come first
   {
     moe_route_cfg rc{MOE_SCORING_SOFTMAX, 1, 1, 1, 1.0f, 0.0f};
