@@ -263,7 +263,7 @@ def route_floor_bench(c, dev, reps):
     P = M._ptr
     ws = torch.empty(c.E * c.H * 2, dtype=torch.uint8, device=dev)
     probe_logits = torch.empty(c.T, c.E, dtype=torch.float32, device=dev)
-    names = ["loop", "mfma_only", "lds_mfma", "x_only", "w_only", "x_from_l2"]
+    names = ["loop", "mfma_only", "lds_mfma", "x_only", "w_only", "x_from_l2", "no_w", "no_x"]
     ev = lambda: torch.cuda.Event(enable_timing=True)
 
     def timed(f):

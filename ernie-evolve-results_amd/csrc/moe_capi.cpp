@@ -719,7 +719,7 @@ int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float sca
 
 int moe_route_probe(int variant, const void* x, const void* w, int T, int H, int E,
                     float* logits, void* ws, size_t ws_bytes, void* stream) {
-  if (variant < MOE_RPROBE_LOOP || variant > MOE_RPROBE_X_L2)
+  if (variant < MOE_RPROBE_LOOP || variant > MOE_RPROBE_NO_X)
     return fail(MOE_ERR_INVALID_ARG, "unknown route probe variant %d", variant);
   if (E != 256 || H != 7168)
     return fail(MOE_ERR_UNSUPPORTED, "route probes run the E = 256, H = 7168 loop only (E=%d, H=%d)",

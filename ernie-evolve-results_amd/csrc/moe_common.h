@@ -75,7 +75,7 @@ hipError_t launch_route_small(const __bf16* x, const __bf16* w, bool split, cons
                               int topk_group, float route_scale, float norm_min, float* logits,
                               int32_t* ids, float* wout, int32_t* counts, int32_t* subcnt,
                               hipStream_t s);
-// K-loop probes of the fused route kernel (E = 256, H = 7168), variants 0-5.
+// K-loop probes of the fused route kernel (E = 256, H = 7168), variants 0-7.
 hipError_t launch_route_probe(int variant, const __bf16* x, const __bf16* w, int T, int H, int E,
                               float* logits, void* ws, hipStream_t s);
 hipError_t launch_offsets(const int32_t* counts, int E, int32_t* offsets, hipStream_t s);

@@ -510,6 +510,8 @@ hipError_t launch_route_probe(int variant, const __bf16* x, const __bf16* w, int
     case 3: MOE_RP(RP_NO_W | RP_NO_LDS | RP_NO_MFMA); break;
     case 4: MOE_RP(RP_NO_X | RP_NO_LDS | RP_NO_MFMA); break;
     case 5: MOE_RP(RP_X_L2); break;
+    case 6: MOE_RP(RP_NO_W); break;
+    case 7: MOE_RP(RP_NO_X); break;
     default: return hipErrorInvalidValue;
   }
 #undef MOE_RP

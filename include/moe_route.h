@@ -338,6 +338,10 @@ int moe_stream_probe(int pattern, const void* src, void* dst, long long nvec, in
  *   MOE_RPROBE_X          the x DMA alone (with the barriers)
  *   MOE_RPROBE_W          the weight loads alone (with the barriers)
  *   MOE_RPROBE_X_L2       the whole loop, x re-read from two L2-resident K steps
+ *   MOE_RPROBE_NO_W       the whole loop without the weight loads (registers
+ *                         loaded once)
+ *   MOE_RPROBE_NO_X       the whole loop without the x DMA (the ring keeps
+ *                         what it holds)
  * x [T,7168] bf16 and w [256,7168] bf16 (16-byte aligned); ws: at least
  * moe_route_workspace_bytes(T, 7168, 256, MOE_DTYPE_BF16) bytes (the
  * fragment-major weight copy, written first).  logits [T,256] fp32 or NULL:
@@ -349,6 +353,8 @@ int moe_stream_probe(int pattern, const void* src, void* dst, long long nvec, in
 #define MOE_RPROBE_X 3
 #define MOE_RPROBE_W 4
 #define MOE_RPROBE_X_L2 5
+#define MOE_RPROBE_NO_W 6
+#define MOE_RPROBE_NO_X 7
 int moe_route_probe(int variant, const void* x, const void* w, int T, int H, int E,
                     float* logits, void* ws, size_t ws_bytes, void* stream);
 

@@ -376,7 +376,7 @@ def test_stream_probe_validation():
 def test_route_probe_validation():
     L = M.lib()
     ws = 256 * 7168 * 2
-    err(L.moe_route_probe(6, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws, None), -2, "variant")
+    err(L.moe_route_probe(8, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws, None), -2, "variant")
     err(L.moe_route_probe(-1, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws, None), -2, "variant")
     err(L.moe_route_probe(0, FAKE, FAKE, 128, 4096, 256, None, FAKE, ws, None), -3, "7168")
     err(L.moe_route_probe(0, FAKE, FAKE, 128, 7168, 128, None, FAKE, ws, None), -3, "7168")

@@ -35,7 +35,7 @@ def test_every_probe_variant_runs(cuda):
     sink = torch.empty(T, c.E, device=cuda)
     L = M.lib()
     s = M._stream(x)
-    for v in range(6):
+    for v in range(8):
         print("route probe variant %d" % v, flush=True)
         M._check(L.moe_route_probe(v, M._ptr(x), M._ptr(w), T, c.H, c.E,
                                    M._ptr(sink) if v % 2 else None, M._ptr(ws), ws.numel(), s))
