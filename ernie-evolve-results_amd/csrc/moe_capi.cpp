@@ -102,10 +102,9 @@ static int route_parts(int T, int H, int E, int w_dtype) {
 size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype) {
   if (T < 0 || H < 0 || E <= 0) return 0;
   if (w_dtype != MOE_DTYPE_BF16 && w_dtype != MOE_DTYPE_FP32) return 0;
-  // E = 8 or 16 (8 with fp32 weights): the small-E GEMM + scoring kernel; no
-  // workspace beyond an fp32 weight's hi/lo split
-  if (moe::route_small_supported(E, H, w_dtype == MOE_DTYPE_FP32))
-    return w_dtype == MOE_DTYPE_FP32 ? round256((size_t)2 * E * H * 2) : 0;
+  // E = 8 or 16 (8 with fp32 weights): the small-E GEMM + scoring kernel, no
+  // workspace (it splits an fp32 weight itself)
+  if (moe::route_small_supported(E, H, w_dtype == MOE_DTYPE_FP32)) return 0;
   const int parts = route_parts(T, H, E, w_dtype);
   size_t b = 0;
   if (w_dtype == MOE_DTYPE_FP32) b += round256((size_t)2 * E * H * 2);
@@ -210,17 +209,8 @@ static int route_launch(const void* x, const void* w, int w_dtype, const float* 
                                      s),
                     "topk");
   if (route_is_small(T, H, E, w_dtype)) {
-    const bool split = w_dtype == MOE_DTYPE_FP32;
-    const __bf16* wb = (const __bf16*)w;
-    if (split) {
-      // fp32 weights: hi/lo bf16 split (K:1786-1824) into the workspace
-      __bf16* wpk = (__bf16*)ws;
-      const int rc = launched(moe::launch_wsplit((const float*)w, wpk, E, H, s), "wsplit");
-      if (rc) return rc;
-      wb = wpk;
-    }
-    return launched(moe::launch_route_small((const __bf16*)x, wb, split, bias, T, E, H, k,
-                                            cfg->scoring, cfg->renormalize, cfg->n_group,
+    return launched(moe::launch_route_small((const __bf16*)x, w, w_dtype == MOE_DTYPE_FP32, bias,
+                                            T, E, H, k, cfg->scoring, cfg->renormalize, cfg->n_group,
                                             cfg->topk_group, cfg->route_scale, cfg->norm_min,
                                             logits, topk_ids, topk_w, counts, blockcnt, s),
                     "route_small");

@@ -63,14 +63,13 @@ hipError_t launch_route_fused(const __bf16* x, const __bf16* w, const float* bia
                               float route_scale, float norm_min, float* logits, int32_t* ids,
                               float* wout, int32_t* counts, int32_t* blockcnt, void* ws,
                               hipStream_t s);
-// The router GEMM + scoring for few experts (route_small.hip): E = 8 or 16
-// with bf16 weights, or E = 8 with split = true (w is an fp32 weight's hi/lo
-// bf16 split [2E, H], launch_wsplit's); H % 256 == 0.  subcnt (or NULL): the
-// block histograms of its route_small_tokens()-token tiles,
-// [E, ceil(T / route_small_tokens())].
-bool route_small_supported(int E, int H, bool split);
+// The router GEMM + scoring for few experts (route_small.hip): w bf16 [E, H]
+// with E = 8 or 16, or (wf32) fp32 [E, H] with E = 8, split hi/lo in the
+// kernel; H % 256 == 0.  subcnt (or NULL): the block histograms of its
+// route_small_tokens()-token tiles, [E, ceil(T / route_small_tokens())].
+bool route_small_supported(int E, int H, bool wf32);
 int route_small_tokens();
-hipError_t launch_route_small(const __bf16* x, const __bf16* w, bool split, const float* bias,
+hipError_t launch_route_small(const __bf16* x, const void* w, bool wf32, const float* bias,
                               int T, int E, int H, int k, int scoring, int renorm, int n_group,
                               int topk_group, float route_scale, float norm_min, float* logits,
                               int32_t* ids, float* wout, int32_t* counts, int32_t* subcnt,

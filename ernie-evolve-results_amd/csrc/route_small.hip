@@ -53,12 +53,15 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & (CH - 1); }
 }  // namespace rs
 
 // NG waves, wave g owning K part g (H / NG, whole 64-wide steps) of all 32
-// tokens, each on its own NS-stage LDS ring.  HL = 2: w is an fp32 weight's
-// hi/lo bf16 split [2E, H] (E = 8: the 16 columns are the 8 hi then the 8 lo
-// rows), and a logit is the sum of 2 * NG partials, hi then lo per K part.
+// tokens, each on its own NS-stage LDS ring.  HL = 1: w is the bf16 weight
+// [E, H].  HL = 2 (E = 8): w is an fp32 weight [E, H]; its rows come into the
+// ring as fp32 and each lane splits its 8 k into hi = bf16(w) and
+// lo = bf16(w - hi) (the reference's wsplit_kernel, K:1786-1824), so the 16
+// fragment columns are the 8 hi then the 8 lo rows, and a logit is the sum of
+// 2 * NG partials, hi then lo per K part.
 template <int E, int V, int KK, int SC, int NG, int NS, int HL>
 __global__ __launch_bounds__(64 * NG) void route_small_kernel(
-    const __bf16* __restrict__ x, const __bf16* __restrict__ w, const float* __restrict__ bias,
+    const __bf16* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
     int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
     float norm_min, float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ wout,
     int* __restrict__ counts, int* __restrict__ subcnt, int nsub) {
@@ -67,11 +70,16 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
   constexpr int NT = 64 * NG;
   static_assert((E == 8 || E == 16) && (HL == 1 || HL == 2) && HL * E <= 16,
                 "one 16-column weight fragment");
-  constexpr int NW = HL * E;    // weight rows
+  constexpr int NW = HL * E;    // weight fragment columns in use
   constexpr int NP = NG * HL;   // partial logit blocks per token
-  // a stage: TB token rows and the NW weight rows, 8 rows x 128 B per DMA instruction
-  constexpr int STAGE_B = (TB + NW) * ROWB;
-  constexpr int NQ = (TB + NW) / RPI;
+  // a stage: TB token rows (128 B each), then the E weight rows of one K step,
+  // 128 B of bf16 (HL = 1) or 256 B of fp32 (HL = 2) each; 1 KB per DMA
+  // instruction (8 token rows, 8 bf16 or 4 fp32 weight rows)
+  constexpr int WROWB = HL == 2 ? 2 * ROWB : ROWB;
+  constexpr int STAGE_B = TB * ROWB + E * WROWB;
+  constexpr int NQX = TB / RPI;
+  constexpr int NQ = NQX + E * WROWB / 1024;
+  static_assert(E * WROWB % 1024 == 0, "whole DMA instructions");
   constexpr int RING_B = NG * NS * STAGE_B;
   constexpr int PART_B = TB * NP * E * 4;
   // the partial tiles reuse the rings once every wave has left its K loop
@@ -86,29 +94,37 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
   const int KT = kw / BK;
   char* const wring = lds + g * NS * STAGE_B;
 
-  // Per-lane source of each DMA instruction of a stage: stage rows [0, TB)
-  // are token rows (past T: a copy of row T-1, never stored), rows
-  // [TB, TB + NW) the weight rows.
-  const __bf16* src[NQ];
+  // Per-lane source of each DMA instruction of a stage (its K step 0): token
+  // rows (past T: a copy of row T-1, never stored) with 16-byte chunk p of row
+  // r at physical chunk p ^ swz(r); then the weight rows, bf16 the same way, or
+  // fp32 with 32-byte chunk c of row e at physical chunk c ^ e.
+  const char* src[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
-    const int r = q * RPI + lane / CH;  // stage row
-    const int p = lane % CH;
-    const __bf16* base;
-    if (r < TB) {
+    if (q < NQX) {
+      const int r = q * RPI + lane / CH;  // stage row
       long long t = m0 + r;
       if (t >= T) t = T - 1;
-      base = x + t * H;
+      src[q] = reinterpret_cast<const char*>(x + t * H + (long long)g * kw +
+                                             ((lane % CH) ^ swz(r)) * 8);
+    } else if constexpr (HL == 1) {
+      const int r = (q - NQX) * RPI + lane / CH;  // weight row
+      src[q] = reinterpret_cast<const char*>(static_cast<const __bf16*>(w) + (long long)r * H +
+                                             (long long)g * kw + ((lane % CH) ^ swz(TB + r)) * 8);
     } else {
-      base = w + (long long)(r - TB) * H;
+      const int e = (q - NQX) * 4 + lane / 16;  // weight row: 16 lanes x 16 B
+      const int pc = (lane % 16) / 2, hf = lane % 2;  // physical 32-byte chunk, its half
+      src[q] = reinterpret_cast<const char*>(static_cast<const float*>(w) + (long long)e * H +
+                                             (long long)g * kw + (pc ^ e) * 8 + hf * 4);
     }
-    src[q] = base + (long long)g * kw + (p ^ swz(r)) * 8;
   }
   auto issue = [&](int kt, int st) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       auto* dst = (__attribute__((address_space(3))) void*)(wring + st * STAGE_B + q * 1024);
-      __builtin_amdgcn_global_load_lds((const void*)(src[q] + kt * BK), dst, 16, 0, 0);
+      const int step_b = (q < NQX || HL == 1) ? BK * 2 : BK * 4;  // bytes per K step
+      __builtin_amdgcn_global_load_lds((const void*)(src[q] + (long long)kt * step_b), dst, 16, 0,
+                                       0);
     }
   };
 
@@ -133,12 +149,33 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
       // lane (fr, fc) feeds k = kk*32 + fc*8 .. +8 of row fr: the standalone
       // GEMM's mapping, so the parts' sums are its K partitions' bit for bit
       const int c = kk * 4 + fc;
-      // the weight fragment's 16 columns: weight row fr % NW (at E = 8 with
-      // one half, columns 8..15 repeat 0..7 and are dropped)
-      const int rb = TB + fr % NW, r1 = 16 + fr;
+      const int r1 = 16 + fr;
       const bf16x8 a0 = *reinterpret_cast<const bf16x8*>(sb + fr * ROWB + ((c ^ swz(fr)) * 16));
       const bf16x8 a1 = *reinterpret_cast<const bf16x8*>(sb + r1 * ROWB + ((c ^ swz(r1)) * 16));
-      const bf16x8 b = *reinterpret_cast<const bf16x8*>(sb + rb * ROWB + ((c ^ swz(rb)) * 16));
+      const char* wb = sb + TB * ROWB;
+      bf16x8 b;
+      if constexpr (HL == 1) {
+        // the weight fragment's 16 columns: weight row fr % E (at E = 8
+        // columns 8..15 repeat 0..7 and are dropped)
+        const int rb = fr % E;
+        b = *reinterpret_cast<const bf16x8*>(wb + rb * ROWB + ((c ^ swz(TB + rb)) * 16));
+      } else {
+        // columns 0..7: hi of row fr, 8..15: lo of row fr - 8, from the same
+        // 8 fp32 (lanes fr and fr + 8 read one address)
+        const int e = fr & 7;
+        const f32x4* pv = reinterpret_cast<const f32x4*>(wb + e * WROWB + (c ^ e) * 32);
+        const f32x4 v0 = pv[0], v1 = pv[1];
+        const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        unsigned int hv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const unsigned int h = f2bf(v[i]);
+          hv[i] = fr < 8 ? h : f2bf(v[i] - __uint_as_float(h << 16));
+        }
+        const u32x4 pk = {hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
+                          hv[6] | (hv[7] << 16)};
+        b = __builtin_bit_cast(bf16x8, pk);
+      }
       acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b, acc0, 0, 0, 0);
       acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b, acc1, 0, 0, 0);
     }
@@ -212,15 +249,16 @@ __global__ void rs_zero_kernel(int* __restrict__ p, int n) {
 }
 
 // H a multiple of 256 (four parts of whole 64-wide K steps); E = 8 or 16 with
-// bf16 weights, E = 8 with an fp32 weight's hi/lo split (16 weight rows).
-bool route_small_supported(int E, int H, bool split) {
-  return (split ? E == 8 : (E == 8 || E == 16)) && H > 0 && H % (rs::NG * rs::BK) == 0;
+// bf16 weights, E = 8 with fp32 weights (split hi/lo in the kernel: 16 weight
+// fragment columns).
+bool route_small_supported(int E, int H, bool wf32) {
+  return (wf32 ? E == 8 : (E == 8 || E == 16)) && H > 0 && H % (rs::NG * rs::BK) == 0;
 }
 
 int route_small_tokens() { return rs::TB; }
 
 template <int E, int V, int KK, int SC, int HL>
-static hipError_t launch_rs(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
+static hipError_t launch_rs(const __bf16* x, const void* w, const float* bias, int T, int H,
                             int k, int renorm, int n_group, int topk_group, float route_scale,
                             float norm_min, float* logits, int32_t* ids, float* wout,
                             int32_t* counts, int32_t* subcnt, hipStream_t s) {
@@ -232,7 +270,7 @@ static hipError_t launch_rs(const __bf16* x, const __bf16* w, const float* bias,
 }
 
 template <int E, int V, int HL>
-static hipError_t launch_rs_cfg(const __bf16* x, const __bf16* w, const float* bias, int T, int H,
+static hipError_t launch_rs_cfg(const __bf16* x, const void* w, const float* bias, int T, int H,
                                 int k, int scoring, int renorm, int n_group, int topk_group,
                                 float route_scale, float norm_min, float* logits, int32_t* ids,
                                 float* wout, int32_t* counts, int32_t* subcnt, hipStream_t s) {
@@ -248,7 +286,7 @@ static hipError_t launch_rs_cfg(const __bf16* x, const __bf16* w, const float* b
 #undef MOE_RS_ARGS
 }
 
-hipError_t launch_route_small(const __bf16* x, const __bf16* w, bool split, const float* bias,
+hipError_t launch_route_small(const __bf16* x, const void* w, bool wf32, const float* bias,
                               int T, int E, int H, int k, int scoring, int renorm, int n_group,
                               int topk_group, float route_scale, float norm_min, float* logits,
                               int32_t* ids, float* wout, int32_t* counts, int32_t* subcnt,
@@ -261,7 +299,7 @@ hipError_t launch_route_small(const __bf16* x, const __bf16* w, bool split, cons
   if (T == 0) return hipSuccess;
   // lanes of min(2, E/8) experts: a sigmoid group holds at least two
   const int V = topk_lane_width(E, scoring, n_group);
-  if (split) {
+  if (wf32) {
     if (E == 8 && V == 1)
       return launch_rs_cfg<8, 1, 2>(x, w, bias, T, H, k, scoring, renorm, n_group, topk_group,
                                     route_scale, norm_min, logits, ids, wout, counts, subcnt, s);

@@ -84,8 +84,8 @@ const char* moe_last_error_string(void);
  *     of the weight, E*H*2 bytes (3.5 MiB / 512 KiB), rewritten by every call.
  * E = 8 or 16 with bf16 weights and H % 256 == 0 (the Mixtral shape): zero;
  * one kernel does the GEMM, with K split across the four waves of a block,
- * and the scoring (E = 8 with FP32 weights: the same kernel on the hi/lo
- * split, so only the [2E,H] split weight).
+ * and the scoring (E = 8 with FP32 weights too: the kernel splits the weight
+ * into its bf16 hi/lo halves itself).
  * The size does not depend on cfg; it covers whichever path the call takes. */
 size_t moe_route_workspace_bytes(int T, int H, int E, int w_dtype);
 

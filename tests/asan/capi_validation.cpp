@@ -63,7 +63,7 @@ int main() {
   // C2 (E = 8, bf16): the small-E GEMM + scoring kernel needs no route workspace; through
   // moe_route_permute it adds its 32-token histograms, 8 experts x 256 columns of int32
   if (moe_route_workspace_bytes(8192, 4096, 8, MOE_DTYPE_BF16) != 0) ++failures;
-  if (moe_route_workspace_bytes(8192, 4096, 8, MOE_DTYPE_FP32) != (size_t)2 * 8 * 4096 * 2) ++failures;
+  if (moe_route_workspace_bytes(8192, 4096, 8, MOE_DTYPE_FP32) != 0) ++failures;
   if (moe_route_permute_workspace_bytes(8192, 4096, 8, 2, MOE_DTYPE_BF16) !=
       moe_permute_fp8_workspace_bytes(8192, 4096, 8, 2) + (size_t)8 * 256 * 4)
     ++failures;

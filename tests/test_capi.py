@@ -125,9 +125,9 @@ def _route_small(H, E, fp32):
 def _route_ws(T, H, E, fp32):
     r256 = lambda b: (b + 255) // 256 * 256
     if _route_small(H, E, fp32):
-        # no K partitions (the four waves of a block split K and add in LDS); fp32
-        # weights still need their [2E, H] bf16 hi/lo split
-        return r256(2 * E * H * 2) if fp32 else 0
+        # no K partitions (the four waves of a block split K and add in LDS), and
+        # an fp32 weight is split hi/lo inside the kernel
+        return 0
     N = 2 * E if fp32 else E
     parts = (N // E) * _router_ksplit(T, H, N)
     b = r256(2 * E * H * 2) if fp32 else 0
@@ -152,9 +152,9 @@ def test_workspace_sizes():
     assert L.moe_route_workspace_bytes(32768, 7168, 256, 1) == 2 * 256 * 7168 * 2 + 32768 * 512 * 4
     assert L.moe_route_workspace_bytes(65536, 7168, 256, 0) == 256 * 7168 * 2
     assert L.moe_route_workspace_bytes(32768, 4096, 256, 0) == 0   # no fused kernel, no K split
-    # C2 (Mixtral) shape: the small-E kernel, no workspace; fp32 weights still split hi/lo
+    # C2 (Mixtral) shape: the small-E kernel, no workspace (with fp32 weights it splits them itself)
     assert L.moe_route_workspace_bytes(8192, 4096, 8, 0) == 0
-    assert L.moe_route_workspace_bytes(8192, 4096, 8, 1) == 2 * 8 * 4096 * 2
+    assert L.moe_route_workspace_bytes(8192, 4096, 8, 1) == 0
     for T, H, E in [(1, 64, 8), (100, 128, 8), (512, 1024, 8), (8192, 4096, 8), (16384, 2048, 128),
                     (300, 2048, 16), (300, 1536, 16), (512, 1024, 16), (100, 448, 8),
                     (1571, 8192, 64), (32768, 7168, 256), (300, 7168, 256), (4096, 8192, 64)]:
