@@ -175,131 +175,6 @@ def layer_bench(Ts, steps, warmup, dispatch="bf16", experts="bf16", cold=True):
     print(json.dumps(line), flush=True)
 
 
-def ceiling_bench(c, dev, reps):
-    """The machine's rate for each stage's byte mix at this configuration's
-    sizes: moe_stream_probe kernels (sequential addresses, the stage's cache
-    policy) timed beside the real stages on the same buffers, both back to
-    back (as in the step) and each after a 1 GiB rewrite.  Prints one JSON
-    line."""
-    x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
-    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, dev, fp8=c.fp8)
-    L = M.lib()
-    stream = M._stream(x)
-    nx = c.T * c.H * 2 // 16            # 16-byte vectors of x (and of out)
-    P = M._ptr
-    # 1 GiB rewrite as 4 streams (its own kernel symbol, apart from the probes)
-    flush = lambda: L.moe_stream_probe(1, None, P(plan.xg), (1 << 30) // 16 // 4, 4, stream)
-    pats = {  # name: (pattern, src, dst, nvec, ways, bytes read, bytes written)
-        "x_read": (0, x, plan.out, nx, 1, nx * 16, 0),
-        "rows_read": (0, y, plan.out, nx, c.k, c.k * nx * 16, 0),
-        "rows_write": (1, None, plan.xg, nx, c.k, 0, c.k * nx * 16),
-        "gather_mix": (2, x, plan.xg, nx, c.k, nx * 16, c.k * nx * 16),
-        "combine_mix": (3, y, plan.out, nx, c.k, c.k * nx * 16, nx * 16),
-        "copy_1GiB": (4, y, plan.xg, (1 << 30) // 16, 1, 1 << 30, 1 << 30),
-    }
-    ev = lambda: torch.cuda.Event(enable_timing=True)
-
-    def timed(f, cold):
-        ts = []
-        for _ in range(reps + 2):
-            if cold:
-                flush()
-            a, b = ev(), ev()
-            a.record()
-            f()
-            b.record()
-            b.synchronize()
-            ts.append(a.elapsed_time(b) * 1e3)
-        return statistics.median(ts[2:])
-
-    out = {}
-    shapes = {"one_pass": 0, "grid_stride": 0x100}  # MOE_PROBE_GRID_STRIDE
-    for name, (pat, src, dst, n, ways, rb, wb) in pats.items():
-        row = {"read_GB": round(rb / 1e9, 3), "write_GB": round(wb / 1e9, 3)}
-        for shape, flag in shapes.items():
-            f = lambda: M._check(L.moe_stream_probe(pat | flag, P(src), P(dst), n, ways, stream))
-            row[shape] = {ctx + "_us": round(timed(f, ctx == "cold"), 1) for ctx in ("warm", "cold")}
-        for ctx in ("warm", "cold"):
-            us = min(row[sh][ctx + "_us"] for sh in shapes)
-            row["best_" + ctx + "_us"] = us
-            row["best_" + ctx + "_TBps"] = round((rb + wb) / (us * 1e-6) / 1e12, 2)
-        out[name] = row
-    # the real stages on the same buffers (same two contexts)
-    plan.step(x, w, bias, y)
-    real = {"route": lambda: plan.route(x, w, bias), "gather": lambda: plan.permute(x),
-            "combine": lambda: plan.combine(y)}
-    ab = algorithmic_bytes(c)
-    rbytes = {"route": ab["route"], "gather": ab["gather"], "combine": ab["combine"]}
-    rr = {}
-    for name, f in real.items():
-        row = {"algorithmic_GB": round(rbytes[name] / 1e9, 3)}
-        for ctx in ("warm", "cold"):
-            us = timed(f, ctx == "cold")
-            row[ctx + "_us"] = round(us, 1)
-            row[ctx + "_TBps"] = round(rbytes[name] / (us * 1e-6) / 1e12, 2)
-        rr[name] = row
-    print(json.dumps({"mode": "ceiling", "config": c.name, "reps": reps,
-                      "note": "warm: back to back; cold: each after a 1 GiB rewrite; probes in "
-                              "both launch shapes, best_* = the faster. gather = moe_permute "
-                              "(index kernels + gather)",
-                      "probes": out, "real": rr,
-                      "probe_floor_warm_us": round(sum(out[n]["best_warm_us"] for n in
-                                                       ("x_read", "gather_mix", "combine_mix")), 1)}),
-          flush=True)
-
-
-def route_floor_bench(c, dev, reps):
-    """What bounds the fused route kernel's K loop: the loop alone and with parts
-    taken out (moe_route_probe, E = 256 and H = 7168 only), beside the real route
-    stage and a plain read of x, all back to back on the same buffers.  Prints
-    one JSON line; `loop_logits_bitexact` checks that the whole-loop probe
-    computes moe_route's logits."""
-    if (c.E, c.H) != (256, 7168):
-        raise SystemExit("--route-floor needs the E = 256, H = 7168 shape (C4 or C5)")
-    x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
-    plan = M.MoePlan(c.T, c.H, c.E, c.k, c.cfg, dev, fp8=c.fp8)
-    L = M.lib()
-    stream = M._stream(x)
-    P = M._ptr
-    ws = torch.empty(c.E * c.H * 2, dtype=torch.uint8, device=dev)
-    probe_logits = torch.empty(c.T, c.E, dtype=torch.float32, device=dev)
-    names = ["loop", "mfma_only", "lds_mfma", "x_only", "w_only", "x_from_l2", "no_w", "no_x"]
-    ev = lambda: torch.cuda.Event(enable_timing=True)
-
-    def timed(f):
-        # `reps` calls back to back between two events, per call; median of 5
-        ts = []
-        for _ in range(6):
-            a, b = ev(), ev()
-            a.record()
-            for _ in range(reps):
-                f()
-            b.record()
-            b.synchronize()
-            ts.append(a.elapsed_time(b) * 1e3 / reps)
-        return round(statistics.median(ts[1:]), 1)
-
-    plan.route(x, w, bias)
-    M._check(L.moe_route_probe(0, P(x), P(w), c.T, c.H, c.E, P(probe_logits), P(ws), ws.numel(),
-                               stream))
-    torch.cuda.synchronize()
-    exact = bool(torch.equal(probe_logits, plan.logits))
-    out = {}
-    for v, name in enumerate(names):
-        out[name] = timed(lambda: M._check(L.moe_route_probe(v, P(x), P(w), c.T, c.H, c.E, None,
-                                                            P(ws), ws.numel(), stream)))
-    out["route_stage"] = timed(lambda: plan.route(x, w, bias))
-    nx = c.T * c.H * 2 // 16
-    out["x_read"] = timed(lambda: M._check(L.moe_stream_probe(0, P(x), P(plan.out), nx, 1,
-                                                              stream)))
-    mfma_pf = 2.0 * c.T * c.H * c.E / (out["mfma_only"] * 1e-6) / 1e15
-    print(json.dumps({"mode": "route_floor", "config": c.name, "reps": reps,
-                      "note": "us per call, calls back to back; probes and route_stage "
-                              "(moe_route) include the 4-5 us weight re-layout launch",
-                      "us": out, "mfma_only_pflops": round(mfma_pf, 3),
-                      "loop_logits_bitexact": exact}), flush=True)
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -314,12 +189,6 @@ def main():
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one plain 1 GiB device copy (untimed), the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
-    ap.add_argument("--ceiling", action="store_true",
-                    help="time plain streaming kernels that move each stage's byte mix "
-                         "(moe_stream_probe) beside the real stages, on the same buffers")
-    ap.add_argument("--route-floor", action="store_true",
-                    help="time the fused route kernel's K loop alone and with parts taken out "
-                         "(moe_route_probe) beside the real route stage")
     ap.add_argument("--layer", nargs="*", type=int, default=None,
                     help="time run() at the reference's workload T values (default: its mix)")
     ap.add_argument("--layer-fp8", action="store_true",
@@ -342,12 +211,6 @@ def main():
 
     c = CONFIGS[args.config]
     dev = torch.device("cuda:0")
-    if args.ceiling:
-        ceiling_bench(c, dev, max(args.steps, 5))
-        return
-    if args.route_floor:
-        route_floor_bench(c, dev, max(args.steps, 5))
-        return
     x, w, bias, y = M.make_inputs(c, seed=0, device=dev)
     # The router takes bf16 hidden states (K:4327-4339); an fp32 config (C1)
     # hands the GPU path bf16(x), cast once here, and keeps its fp32 router
@@ -366,19 +229,39 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    # ---- timed region: exactly K steps, whole path, inputs resident in HBM
+    # ---- timed region: exactly K steps, whole path, inputs resident in HBM.
+    # Each step runs cold: before it, a 1 GiB buffer is rewritten (outside the
+    # step's HIP events), evicting L2 and the 256 MB MALL, so no step finds the
+    # previous one's data in the caches.  ms_per_step = the median of the K
+    # event-timed steps.
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    evs = [(ev(), ev()) for _ in range(args.steps)]
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
+    for e0, e1 in evs:
+        flush.fill_(1)
+        e0.record()
+        plan.step(x, w, bias, y)
+        e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    cold = [e0.elapsed_time(e1) for e0, e1 in evs]
+    ms_per_step = statistics.median(cold)
+    del flush
+
+    # ---- the same K steps back to back (no rewrite between them): wall clock
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
     for _ in range(args.steps):
         plan.step(x, w, bias, y)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_per_step = wall * 1e3 / args.steps
+    warm_ms = (time.perf_counter() - t1) * 1e3 / args.steps
 
     # ---- per-stage HIP-event timing (on the stream the kernels run on).
     # permute = index kernels + the gather launch; an index-only permute (no
     # rows) isolates the gather.  route = the router GEMM and the scoring (one
     # fused kernel at the DeepSeek-V3 shape, plus its weight re-layout pass).
-    ev = lambda: torch.cuda.Event(enable_timing=True)
     st = {"route": [], "permute": [], "permute_index": [], "combine": []}
     for _ in range(args.steps):
         e = [ev() for _ in range(5)]
@@ -398,20 +281,6 @@ def main():
         st["permute_index"].append(e[3].elapsed_time(e[4]) * 1e3)
     us = {k2: statistics.mean(v) for k2, v in st.items()}
 
-    # ---- cold-cache step: 20 single steps, each after a 1 GiB rewrite that
-    # evicts L2 and the MALL (reported beside `value`, which is the K-step rate)
-    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    cold = []
-    for _ in range(20):
-        flush.fill_(1)
-        e0, e1 = ev(), ev()
-        e0.record()
-        plan.step(x, w, bias, y)
-        e1.record()
-        e1.synchronize()
-        cold.append(e0.elapsed_time(e1))
-    del flush
-    cold_ms = statistics.median(cold)
     us["gather"] = us["permute"] - us["permute_index"]
 
     ab = algorithmic_bytes(c)
@@ -460,8 +329,15 @@ def main():
             "gather": round(ab["gather"] / (us["gather"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "combine": round(ab["combine"] / (us["combine"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
         "route_mfma": route,
-        "cold_step": {"ms": round(cold_ms, 4), "tokens_per_s": round(c.T / (cold_ms * 1e-3), 1),
-                      "note": "median of 20 single steps, each after a 1 GiB rewrite (L2 + MALL)"},
+        "timing": {"protocol": "value and ms_per_step: median of the K steps, each timed with HIP "
+                               "events after a 1 GiB rewrite (cold L2 and MALL)",
+                   "cold_steps_ms": {"median": round(ms_per_step, 4), "min": round(min(cold), 4),
+                                     "max": round(max(cold), 4)},
+                   "timed_region_wall_s": round(wall, 4),
+                   "back_to_back": {"ms_per_step": round(warm_ms, 4),
+                                    "tokens_per_s": round(c.T / (warm_ms * 1e-3), 1),
+                                    "note": "the same K steps with no rewrite between them "
+                                            "(wall clock)"}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

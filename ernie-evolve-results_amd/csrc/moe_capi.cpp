@@ -241,7 +241,9 @@ static int route_launch(const void* x, const void* w, int w_dtype, const float* 
   rc = launched(moe::launch_router_gemm((const __bf16*)x, wb, T, H, N, ksplit, gout, s),
                 "router_gemm");
   if (rc) return rc;
-  return launched(moe::launch_topk(gout, parts, bias, T, E, k, cfg->scoring, cfg->renormalize,
+  // an fp32 weight's partials fold as (sum of hi) + (sum of lo): negative count
+  const int fold = w_dtype == MOE_DTYPE_FP32 ? -parts : parts;
+  return launched(moe::launch_topk(gout, fold, bias, T, E, k, cfg->scoring, cfg->renormalize,
                                    cfg->n_group, cfg->topk_group, cfg->route_scale,
                                    cfg->norm_min, parts > 1 ? logits : nullptr, topk_ids, topk_w,
                                    counts, blockcnt, s),
@@ -705,43 +707,6 @@ int moe_quant_rows_i8(const void* x, long long R, int K, int hadamard, float sca
                                             group_rows, group_counts, (signed char*)q, scales,
                                             (hipStream_t)stream),
                   "quant_rows_i8");
-}
-
-int moe_route_probe(int variant, const void* x, const void* w, int T, int H, int E,
-                    float* logits, void* ws, size_t ws_bytes, void* stream) {
-  if (variant < MOE_RPROBE_LOOP || variant > MOE_RPROBE_NO_X)
-    return fail(MOE_ERR_INVALID_ARG, "unknown route probe variant %d", variant);
-  if (E != 256 || H != 7168)
-    return fail(MOE_ERR_UNSUPPORTED, "route probes run the E = 256, H = 7168 loop only (E=%d, H=%d)",
-                E, H);
-  if (T < 1 || T > (1 << 24)) return fail(MOE_ERR_INVALID_ARG, "T=%d not in [1, 2^24]", T);
-  if (!x || !w) return fail(MOE_ERR_NULL_POINTER, "x and w are required");
-  const size_t need = moe::route_fused_workspace_bytes(E, H);
-  if (!ws || ws_bytes < need)
-    return fail(MOE_ERR_WORKSPACE, "workspace %zu bytes < %zu required", ws ? ws_bytes : 0, need);
-  if (!aligned16(x) || !aligned16(w) || !aligned16(ws))
-    return fail(MOE_ERR_ALIGNMENT, "x, w and ws must be 16-byte aligned");
-  return launched(moe::launch_route_probe(variant, (const __bf16*)x, (const __bf16*)w, T, H, E,
-                                          logits, ws, (hipStream_t)stream),
-                  "route_probe");
-}
-
-int moe_stream_probe(int pattern, const void* src, void* dst, long long nvec, int ways,
-                     void* stream) {
-  const int base = pattern & ~MOE_PROBE_GRID_STRIDE;
-  if (base < MOE_PROBE_READ || base > MOE_PROBE_COPY)
-    return fail(MOE_ERR_INVALID_ARG, "unknown probe pattern %d", pattern);
-  if (nvec < 0) return fail(MOE_ERR_INVALID_ARG, "nvec=%lld < 0", nvec);
-  if (base != MOE_PROBE_COPY && (ways < 1 || ways > 8))
-    return fail(MOE_ERR_INVALID_ARG, "ways=%d not in [1, 8]", ways);
-  if (nvec > (1LL << 39)) return fail(MOE_ERR_INVALID_ARG, "nvec=%lld too large", nvec);
-  if (!dst || (base != MOE_PROBE_WRITE && !src))
-    return fail(MOE_ERR_NULL_POINTER, "src and dst are required");
-  if (!aligned16(dst) || (src && !aligned16(src)))
-    return fail(MOE_ERR_ALIGNMENT, "src and dst must be 16-byte aligned");
-  if (nvec == 0) return ok();
-  return launched(moe::launch_stream_probe(pattern, src, dst, nvec, ways, (hipStream_t)stream),
-                  "stream_probe");
 }
 
 }  // extern "C"

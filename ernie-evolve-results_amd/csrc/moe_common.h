@@ -74,9 +74,6 @@ hipError_t launch_route_small(const __bf16* x, const void* w, bool wf32, const f
                               int topk_group, float route_scale, float norm_min, float* logits,
                               int32_t* ids, float* wout, int32_t* counts, int32_t* subcnt,
                               hipStream_t s);
-// K-loop probes of the fused route kernel (E = 256, H = 7168), variants 0-7.
-hipError_t launch_route_probe(int variant, const __bf16* x, const __bf16* w, int T, int H, int E,
-                              float* logits, void* ws, hipStream_t s);
 hipError_t launch_offsets(const int32_t* counts, int E, int32_t* offsets, hipStream_t s);
 hipError_t launch_dispatch_index(const int32_t* ids, int T, int E, int k, int32_t* blockcnt,
                                  int32_t* totals, int32_t* row_token, int32_t* pair_row,
@@ -123,9 +120,6 @@ hipError_t launch_quant_rows_i8(const __bf16* x, long long R, int K, int had, fl
                                 int group_rows, const int* counts, signed char* q, float* s,
                                 hipStream_t st);
 
-// Streaming probes of the stage byte mixes (pattern: MOE_PROBE_*).
-hipError_t launch_stream_probe(int pattern, const void* src, void* dst, long long nvec, int ways,
-                               hipStream_t s);
 
 // Experts per lane of the scoring kernel for (E, scoring, n_group).
 int topk_lane_width(int E, int scoring, int n_group);

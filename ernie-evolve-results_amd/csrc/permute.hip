@@ -195,7 +195,9 @@ hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, const int32
                      (const u32x4*)x, pair_row, nchunks, cpr, nb, k, (u32x4*)xg, scales, stage);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !stage) return e;
-  const bool vec = nb % 4 == 0;
+  // 16-byte pieces only where every piece is 16-byte aligned in both buffers
+  // (scales needs only 4-byte alignment at the C ABI)
+  const bool vec = nb % 4 == 0 && ((uintptr_t)scales & 15u) == 0 && ((uintptr_t)stage & 15u) == 0;
   const long long nitems = (long long)T * k * (vec ? nb / 4 : nb);
   const dim3 sgrid((unsigned)((nitems + 256LL * kScatterItems - 1) / (256LL * kScatterItems)));
   if (vec)

@@ -96,13 +96,7 @@ constexpr int route_fused_lds(int BM, int E, int D) {
 // flight.  KTC: the K steps, fully unrolled.  V, KK, SC: the scoring lane
 // width, k (0: runtime) and rule.  NTOK: tokens one lane group scores per pass.
 // nt_from: the first tile whose x loads are non-temporal (rf_temporal_tiles).
-// PROBE (0 in the library's route): a measurement build of the K loop alone
-// with parts of it taken out (the RP_* bits); it skips the epilogue and, with
-// logits != NULL, writes the raw fp32 tile as [T, E] logits.
-constexpr int RP_ON = 1, RP_X_L2 = 2, RP_NO_X = 4, RP_NO_W = 8, RP_NO_LDS = 16, RP_NO_MFMA = 32,
-              RP_NO_BAR = 64;
-template <int BM, int E, int NWV, int D, int KTC, int V, int KK, int SC, int NTOK,
-          int PROBE = 0>
+template <int BM, int E, int NWV, int D, int KTC, int V, int KK, int SC, int NTOK>
 __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
     const __bf16* __restrict__ x, const __bf16* __restrict__ wf, const float* __restrict__ bias,
     int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
@@ -151,9 +145,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
       auto* dst = (__attribute__((address_space(3))) void*)(st + (wave * NX + q) * 1024);
       // tiles from nt_from on: non-temporal (aux bit 1: nt), so they do not
       // displace the rows of the earlier tiles from the memory-side cache
-      // (probe RP_X_L2: every step re-reads one of the first two K steps,
-      // which stay in L2)
-      const int sk = (PROBE & RP_X_L2) ? (src_kt & 1) : src_kt;
+      const int sk = src_kt;
       if ((int)blockIdx.x >= nt_from)
         __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + sk * BK), dst, 16, 0, 2);
       else
@@ -169,8 +161,7 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
         dst[kk * NJ + j] = *reinterpret_cast<const bf16x8*>(
             wf + ((long long)((kt * 2 + kk) * (E / 16) + wg * NJ + j) * 64 + lane) * 8);
   };
-  constexpr int VMW =
-      (D - 1) * (((PROBE & RP_NO_X) ? 0 : NX) + ((PROBE & RP_NO_W) ? 0 : NWF));
+  constexpr int VMW = (D - 1) * (NX + NWF);
 
   f32x4 acc[FM][NJ];
 #pragma unroll
@@ -189,7 +180,6 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
   // reload step KT-1 into slots nobody reads again, so the compiler sees one
   // uniform sequence and the vmcnt count below holds on every step.
   bf16x8 a0[FM], a1[FM];
-  unsigned sink = 0u;  // probe RP_NO_MFMA: keeps the weight loads alive
 #pragma unroll
   for (int kb = 0; kb < KT; kb += D) {
 #pragma unroll
@@ -198,80 +188,42 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
       // stage kt and weights kt are the oldest loads once at most (D-1)
       // later steps' loads are pending.  The wait is the builtin, not asm,
       // so the compiler's own vmcnt bookkeeping knows they are retired.
-      // (a probe with its MFMAs taken out would otherwise have its loads
-      // hoisted across steps)
-      if constexpr (PROBE != 0) __builtin_amdgcn_sched_barrier(0);
-      if (!(PROBE & RP_NO_BAR) || kt == 0) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_only(VMW));
-        __builtin_amdgcn_s_barrier();
-      }
+      __builtin_amdgcn_s_waitcnt(vmcnt_only(VMW));
+      __builtin_amdgcn_s_barrier();
       const char* sb = lds + (kt % NS) * STAGE_B;
       // refill x first: stage kt + D goes to the slot of stage kt - 1, which
       // every wave finished reading before this step's barrier, so its DMA can
       // start before this step's fragment reads and MFMAs
       const int kn = kt + D < KT ? kt + D : KT - 1;
-      if constexpr (!(PROBE & RP_NO_X)) issue_x(kt + D, kn);
+      issue_x(kt + D, kn);
       // rows i*16 + fr share the swizzle of fr: a half step's FM fragment
       // reads are 2 KB apart
       auto frag_addr = [&](int kk) {
         return (unsigned)(uintptr_t)((__attribute__((address_space(3))) const char*)(
             sb + fr * ROWB + (((kk * 4 + fc) ^ swz(fr)) * 16)));
       };
-      constexpr bool lds_reads = !(PROBE & RP_NO_LDS);
-      if (lds_reads || kt == 0) {
-        lds_readn<FM>(a0, frag_addr(0));
-        lds_wait<FM>(a0);
-        // the second half's reads go out before the first half's MFMAs and
-        // land while they run
-        lds_readn<FM>(a1, frag_addr(1));
-      }
+      lds_readn<FM>(a0, frag_addr(0));
+      lds_wait<FM>(a0);
+      // the second half's reads go out before the first half's MFMAs and
+      // land while they run
+      lds_readn<FM>(a1, frag_addr(1));
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (!(PROBE & RP_NO_MFMA)) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-          for (int j = 0; j < NJ; ++j)
-            acc[i][j] =
-                __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], wr[u][j], acc[i][j], 0, 0, 0);
-      }
-      {
-        __builtin_amdgcn_sched_barrier(0);
-        if (lds_reads || kt == 0) lds_wait<FM>(a1);
-        if constexpr (!(PROBE & RP_NO_MFMA)) {
-#pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], wr[u][NJ + j],
-                                                                   acc[i][j], 0, 0, 0);
-        } else {
-#pragma unroll
-          for (int q = 0; q < NWF; ++q) {
-            const u32x4 v = __builtin_bit_cast(u32x4, wr[u][q]);
-            sink ^= v[0] ^ v[1] ^ v[2] ^ v[3];
-          }
-        }
-      }
-      // refill the weights of step kt + D once this step's MFMAs have read them
-      if constexpr (!(PROBE & RP_NO_W)) issue_w(kn, wr[u]);
-    }
-  }
-
-  if constexpr (PROBE != 0) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (sink == 0x9e3779b9u) logits[0] = 0.0f;  // kept: the folded loads stay live
-    if (logits) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], wr[u][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      lds_wait<FM>(a1);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const long long t = m0 + i * 16 + fc * 4 + r;
-            if (t < T) logits[t * E + wg * WE + j * 16 + fr] = acc[i][j][r];
-          }
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], wr[u][NJ + j], acc[i][j], 0, 0, 0);
+      // refill the weights of step kt + D once this step's MFMAs have read them
+      issue_w(kn, wr[u]);
     }
-    return;
   }
 
   // ---- epilogue: the fp32 tile through LDS
@@ -483,39 +435,6 @@ static hipError_t launch_rf_cfg(const __bf16* x, const __bf16* wf, const float* 
   MOE_RF_SC(kScoreSoftmaxBias)
 #undef MOE_RF_SC
 #undef MOE_RF_ARGS
-}
-
-// The K-loop probes (measurement aid): the shipped E = 256, H = 7168 loop with
-// parts taken out.  variant: 0 full loop, 1 MFMAs only, 2 LDS reads + barriers
-// + MFMAs (no global loads), 3 x only, 4 weights only, 5 full loop with x from
-// L2.  logits (or NULL): the raw tile.
-hipError_t launch_route_probe(int variant, const __bf16* x, const __bf16* w, int T, int H, int E,
-                              float* logits, void* ws, hipStream_t s) {
-  if (E != 256 || H != 112 * rf::BK || T <= 0) return hipErrorInvalidValue;
-  __bf16* wf = (__bf16*)ws;
-  const int n = E * H / 8;
-  hipLaunchKernelGGL(rf_wfrag_kernel, dim3((n + 255) / 256), dim3(256), 0, s, (const u32x4*)w, H,
-                     E / 16, (u32x4*)wf, n);
-  const dim3 grid((unsigned)((T + 127) / 128)), blk(64 * kRfWaves);
-  const int ntf = rf_temporal_tiles(128, H);
-#define MOE_RP(BITS)                                                                            \
-  hipLaunchKernelGGL((route_fused_kernel<128, 256, kRfWaves, kRfDepth, 112, 32, 8,               \
-                                         kScoreSigmoidGroup, kRfScoreTokens, RP_ON | (BITS)>),   \
-                     grid, blk, 0, s, x, wf, nullptr, T, H, 8, 1, 8, 4, 1.0f, 0.0f, logits,       \
-                     nullptr, nullptr, nullptr, nullptr, 0, 31, ntf)
-  switch (variant) {
-    case 0: MOE_RP(0); break;
-    case 1: MOE_RP(RP_NO_X | RP_NO_W | RP_NO_LDS | RP_NO_BAR); break;
-    case 2: MOE_RP(RP_NO_X | RP_NO_W); break;
-    case 3: MOE_RP(RP_NO_W | RP_NO_LDS | RP_NO_MFMA); break;
-    case 4: MOE_RP(RP_NO_X | RP_NO_LDS | RP_NO_MFMA); break;
-    case 5: MOE_RP(RP_X_L2); break;
-    case 6: MOE_RP(RP_NO_W); break;
-    case 7: MOE_RP(RP_NO_X); break;
-    default: return hipErrorInvalidValue;
-  }
-#undef MOE_RP
-  return hipGetLastError();
 }
 
 // x [T, H] bf16, w [E, H] bf16; ws: route_fused_workspace_bytes(E, H) bytes

@@ -57,8 +57,9 @@ __device__ __forceinline__ int swz(int r) { return (r >> 1) & (CH - 1); }
 // [E, H].  HL = 2 (E = 8): w is an fp32 weight [E, H]; its rows come into the
 // ring as fp32 and each lane splits its 8 k into hi = bf16(w) and
 // lo = bf16(w - hi) (the reference's wsplit_kernel, K:1786-1824), so the 16
-// fragment columns are the 8 hi then the 8 lo rows, and a logit is the sum of
-// 2 * NG partials, hi then lo per K part.
+// fragment columns are the 8 hi then the 8 lo rows, and a logit is
+// (sum of the NG hi partials) + (sum of the NG lo partials), each in K order:
+// the reference's fold of the full hi and lo products.
 template <int E, int V, int KK, int SC, int NG, int NS, int HL>
 __global__ __launch_bounds__(64 * NG) void route_small_kernel(
     const __bf16* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
@@ -72,6 +73,7 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
                 "one 16-column weight fragment");
   constexpr int NW = HL * E;    // weight fragment columns in use
   constexpr int NP = NG * HL;   // partial logit blocks per token
+  constexpr int NPF = HL == 2 ? -NP : NP;  // their fold (fold_parts): hi sum + lo sum
   // a stage: TB token rows (128 B each), then the E weight rows of one K step,
   // 128 B of bf16 (HL = 1) or 256 B of fp32 (HL = 2) each; 1 KB per DMA
   // instruction (8 token rows, 8 bf16 or 4 fp32 weight rows)
@@ -211,12 +213,7 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
     const float* row = part + tl * NP * E;
     float l[1][V];
 #pragma unroll
-    for (int j = 0; j < V; ++j) {
-      float v = row[e0 + j];
-#pragma unroll
-      for (int p = 1; p < NP; ++p) v = v + row[p * E + e0 + j];
-      l[0][j] = v;
-    }
+    for (int j = 0; j < V; ++j) l[0][j] = fold_parts<E>(row + e0 + j, NPF);
     const bool valid[1] = {t < T};
     if (valid[0]) {
 #pragma unroll
@@ -225,7 +222,7 @@ __global__ __launch_bounds__(64 * NG) void route_small_kernel(
     const float* const rows[1] = {row};
     int my_id[1];
     float wv[1];
-    score_tokens<E, V, KK, SC, 1>(l, bl, rows, NP, valid, gl, k_rt, renorm, n_group, topk_group,
+    score_tokens<E, V, KK, SC, 1>(l, bl, rows, NPF, valid, gl, k_rt, renorm, n_group, topk_group,
                                   route_scale, norm_min, my_id, wv);
     if (valid[0] && gl < k) {
       ids[t * k + gl] = my_id[0];

@@ -104,10 +104,32 @@ __device__ __forceinline__ void store_vec(float* __restrict__ p, const float (&v
   }
 }
 
+// One logit from its partial blocks (E floats apart).  nparts > 0: the
+// blocks added in index order.  nparts < 0: -nparts blocks of an fp32
+// weight's bf16 hi/lo split, a (hi, lo) pair per K partition; the logit is
+// (sum of the hi blocks) + (sum of the lo blocks), each in K order: the
+// reference's fold of the two whole half products (K:1786-1824).
+template <int E>
+__device__ __forceinline__ float fold_parts(const float* src, int nparts) {
+#pragma clang fp contract(off)
+  if (nparts > 0) {
+    float v = src[0];
+    for (int p = 1; p < nparts; ++p) v = v + src[p * E];
+    return v;
+  }
+  float hi = src[0], lo = src[E];
+  for (int p = 2; p < -nparts; p += 2) {
+    hi = hi + src[p * E];
+    lo = lo + src[(p + 1) * E];
+  }
+  return hi + lo;
+}
+
 // NT tokens' scores at once, each held by G = E/V consecutive lanes (lane gl
 // of a token owns experts [gl*V, gl*V + V)).  Token n: l[n] the lane's
-// logits, row[n] its logit row (nparts partial blocks of E floats side by
-// side, read only to recompute a selected expert's sigmoid weight), valid[n]
+// logits, row[n] its logit row (|nparts| partial blocks of E floats side by
+// side, folded by fold_parts; read only to recompute a selected expert's
+// sigmoid weight), valid[n]
 // false for a padding token; b: the lane's bias.  Lanes gl < k return slot
 // gl's expert in id_out[n] and its weight in w_out[n].  Every lane of the
 // token's G must call it (cross-lane reductions).
@@ -307,10 +329,7 @@ __device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const floa
     for (int n = 0; n < NT; ++n) {
       my_aux[n] = 0.0f;
       if (valid[n] && gl < k) {
-        const float* src = row[n] + my_id[n];
-        float lv = src[0];
-        for (int p = 1; p < nparts; ++p) lv = lv + src[p * E];
-        my_aux[n] = det_sigmoid(lv);
+        my_aux[n] = det_sigmoid(fold_parts<E>(row[n] + my_id[n], nparts));
       }
     }
     const int base = (threadIdx.x & 63) - gl;

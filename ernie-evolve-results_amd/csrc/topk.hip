@@ -51,19 +51,38 @@ __global__ __launch_bounds__(NT) void topk_kernel(
   const bool valid = t < T;
   const int e0 = gl * V;
   float l[V];
+  const int np = nparts < 0 ? -nparts : nparts;
   {
-    // nparts > 1: the row holds nparts partial sums of the logits side by
-    // side (bf16 hi/lo weight halves, K partitions of the GEMM); they are
-    // added in index order.
-    const int in_stride = nparts * E;
+    // |nparts| > 1: the row holds the partial sums of the logits side by side
+    // (K partitions of the GEMM); nparts > 1: added in index order;
+    // nparts < 0: (hi, lo) pairs of an fp32 weight's bf16 split per K
+    // partition, folded as (sum of hi) + (sum of lo) (fold_parts)
+    const int in_stride = np * E;
     if (valid) {
       const float* src = logits + t * in_stride + e0;
       load_vec<V>(src, l);
-      for (int p = 1; p < nparts; ++p) {
-        float q[V];
-        load_vec<V>(src + p * E, q);
+      if (nparts > 0) {
+        for (int p = 1; p < np; ++p) {
+          float q[V];
+          load_vec<V>(src + p * E, q);
 #pragma unroll
-        for (int j = 0; j < V; ++j) l[j] = l[j] + q[j];
+          for (int j = 0; j < V; ++j) l[j] = l[j] + q[j];
+        }
+      } else {
+        float lo[V];
+        load_vec<V>(src + E, lo);
+        for (int p = 2; p < np; p += 2) {
+          float q[V], r[V];
+          load_vec<V>(src + p * E, q);
+          load_vec<V>(src + (p + 1) * E, r);
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            l[j] = l[j] + q[j];
+            lo[j] = lo[j] + r[j];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) l[j] = l[j] + lo[j];
       }
       if (lout) store_vec<V>(lout + t * E + e0, l);
     } else {
@@ -76,7 +95,7 @@ __global__ __launch_bounds__(NT) void topk_kernel(
   for (int j = 0; j < V; ++j) b[j] = bias ? bias[e0 + j] : 0.0f;
   int my_id;
   float wv;
-  score_token<E, V, KK, SC>(l, b, logits + (valid ? t : 0) * (long long)(nparts * E), nparts,
+  score_token<E, V, KK, SC>(l, b, logits + (valid ? t : 0) * (long long)(np * E), nparts,
                             valid, gl, k_rt, renorm, n_group, topk_group, route_scale, norm_min,
                             my_id, wv);
   {

@@ -35,8 +35,8 @@ EXPORTS = ["moe_version", "moe_last_error_string", "moe_route_workspace_bytes",
            "moe_grouped_gemm_fp8", "moe_grouped_swiglu_fp8", "moe_quant_rows_i8",
            "moe_grouped_gemm_i8", "moe_grouped_swiglu_i8", "moe_grouped_gemm_rows",
            "moe_grouped_swiglu_rows", "moe_permute_noalloc_max_scratch_bytes",
-           "moe_permute_noalloc", "moe_stream_probe", "moe_route_permute_workspace_bytes",
-           "moe_route_permute", "moe_route_probe", "moe_permute_fp8_workspace_bytes"]
+           "moe_permute_noalloc", "moe_route_permute_workspace_bytes",
+           "moe_route_permute", "moe_permute_fp8_workspace_bytes"]
 
 
 class MoeError(RuntimeError):
@@ -98,10 +98,6 @@ def lib():
         L.moe_route_permute.restype = _I
         L.moe_route_permute.argtypes = [_P, _P, _I, _P, _I, _I, _I, _I, ctypes.POINTER(_Cfg), _P,
                                         _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _Z, _P]
-        L.moe_stream_probe.restype = _I
-        L.moe_route_probe.restype = _I
-        L.moe_route_probe.argtypes = [_I, _P, _P, _I, _I, _I, _P, _P, _Z, _P]
-        L.moe_stream_probe.argtypes = [_I, _P, _P, ctypes.c_longlong, _I, _P]
         L.moe_combine.restype = _I
         L.moe_combine.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _P, _P]
         L.moe_grouped_gemm_workspace_bytes.restype = _Z

@@ -17,7 +17,7 @@ LIB_NAME = "libmoe_route.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
 
 SOURCES = ["router_gemm.hip", "topk.hip", "route_fused.hip", "route_small.hip", "dispatch.hip",
-           "permute.hip", "combine.hip", "grouped_gemm.hip", "quant_i8.hip", "stream_probe.hip", "moe_capi.cpp"]
+           "permute.hip", "combine.hip", "grouped_gemm.hip", "quant_i8.hip", "moe_capi.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")

@@ -303,61 +303,6 @@ int moe_grouped_swiglu_i8(const int8_t* a, const float* a_scales, const int32_t*
                           const int8_t* ident_a, const float* ident_scales, int ident_m, void* h,
                           void* ws, size_t ws_bytes, void* stream);
 
-/* Measurement aid, no counterpart in the reference: streaming kernels that move
- * the byte mixes of the HBM-bound stages with sequential addresses (16 bytes per
- * lane, the cache policies of the stage each models), to measure what this GPU
- * sustains for each mix beside the real kernels (bench.py --ceiling).
- *   MOE_PROBE_READ        read `ways` streams src[j*nvec + i] (dst: a 16-byte sink)
- *   MOE_PROBE_WRITE       write `ways` streams dst[j*nvec + i]
- *   MOE_PROBE_GATHER_MIX  read nvec vectors of src, write each to `ways`
- *                         sequential streams dst[j*nvec + i] (dst: ways*nvec)
- *   MOE_PROBE_COMBINE_MIX read `ways` streams src[j*nvec + i] (src: ways*nvec),
- *                         write their bf16 sum to dst[i]
- *   MOE_PROBE_COPY        dst[i] = src[i]
- * ways in [1, 8]; pointers 16-byte aligned; vectors are 16 bytes.  The default
- * launch is one pass (a 256-thread block per 256 vectors); OR-ing
- * MOE_PROBE_GRID_STRIDE into `pattern` runs the same mix as a grid-stride loop
- * over at most 65536 blocks (neither shape is fastest for every mix). */
-#define MOE_PROBE_READ 0
-#define MOE_PROBE_WRITE 1
-#define MOE_PROBE_GATHER_MIX 2
-#define MOE_PROBE_COMBINE_MIX 3
-#define MOE_PROBE_COPY 4
-#define MOE_PROBE_GRID_STRIDE 0x100
-int moe_stream_probe(int pattern, const void* src, void* dst, long long nvec, int ways,
-                     void* stream);
-
-/* Measurement aid, no counterpart in the reference: the fused route kernel's
- * K loop alone (E = 256, H = 7168: 128-token tiles, 8 waves, 4 K steps of
- * loads in flight, the library's x cache policy), no epilogue, with parts of
- * it taken out, to measure what bounds it (bench.py --route-floor):
- *   MOE_RPROBE_LOOP       the whole loop: x DMA, weight loads, LDS fragment
- *                         reads, barriers, MFMAs
- *   MOE_RPROBE_MFMA_ONLY  MFMAs only (fragments and weights loaded once)
- *   MOE_RPROBE_LDS_MFMA   LDS fragment reads, barriers and MFMAs, no global loads
- *   MOE_RPROBE_X          the x DMA alone (with the barriers)
- *   MOE_RPROBE_W          the weight loads alone (with the barriers)
- *   MOE_RPROBE_X_L2       the whole loop, x re-read from two L2-resident K steps
- *   MOE_RPROBE_NO_W       the whole loop without the weight loads (registers
- *                         loaded once)
- *   MOE_RPROBE_NO_X       the whole loop without the x DMA (the ring keeps
- *                         what it holds)
- * x [T,7168] bf16 and w [256,7168] bf16 (16-byte aligned); ws: at least
- * moe_route_workspace_bytes(T, 7168, 256, MOE_DTYPE_BF16) bytes (the
- * fragment-major weight copy, written first).  logits [T,256] fp32 or NULL:
- * the raw accumulator tile; for MOE_RPROBE_LOOP it equals moe_route's logits
- * bit for bit, for the other variants its values carry no meaning. */
-#define MOE_RPROBE_LOOP 0
-#define MOE_RPROBE_MFMA_ONLY 1
-#define MOE_RPROBE_LDS_MFMA 2
-#define MOE_RPROBE_X 3
-#define MOE_RPROBE_W 4
-#define MOE_RPROBE_X_L2 5
-#define MOE_RPROBE_NO_W 6
-#define MOE_RPROBE_NO_X 7
-int moe_route_probe(int variant, const void* x, const void* w, int T, int H, int E,
-                    float* logits, void* ws, size_t ws_bytes, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

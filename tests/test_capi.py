@@ -358,36 +358,6 @@ def test_permute_noalloc_validation():
     err(perm(T=T_max + 1, H=7168, E=256, k=8), -3, "scratch")
 
 
-def test_stream_probe_validation():
-    L = M.lib()
-    err(L.moe_stream_probe(9, FAKE, FAKE, 16, 1, None), -2, "pattern")
-    err(L.moe_stream_probe(2, FAKE, FAKE, 16, 9, None), -2, "ways")
-    err(L.moe_stream_probe(0, None, FAKE, 16, 1, None), -1)
-    err(L.moe_stream_probe(1, None, None, 16, 1, None), -1)
-    err(L.moe_stream_probe(4, ctypes.c_void_p(0x10008), FAKE, 16, 1, None), -6)
-    err(L.moe_stream_probe(0, FAKE, FAKE, -1, 1, None), -2)
-    err(L.moe_stream_probe(0x105, FAKE, FAKE, 16, 1, None), -2, "pattern")
-    err(L.moe_stream_probe(0x200, FAKE, FAKE, 16, 1, None), -2, "pattern")
-    err(L.moe_stream_probe(0x100, FAKE, FAKE, 1 << 40, 1, None), -2, "too large")
-    assert L.moe_stream_probe(0x101, None, FAKE, 0, 1, None) == 0
-    assert L.moe_stream_probe(1, None, FAKE, 0, 1, None) == 0
-
-
-def test_route_probe_validation():
-    L = M.lib()
-    ws = 256 * 7168 * 2
-    err(L.moe_route_probe(8, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws, None), -2, "variant")
-    err(L.moe_route_probe(-1, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws, None), -2, "variant")
-    err(L.moe_route_probe(0, FAKE, FAKE, 128, 4096, 256, None, FAKE, ws, None), -3, "7168")
-    err(L.moe_route_probe(0, FAKE, FAKE, 128, 7168, 128, None, FAKE, ws, None), -3, "7168")
-    err(L.moe_route_probe(0, FAKE, FAKE, 0, 7168, 256, None, FAKE, ws, None), -2)
-    err(L.moe_route_probe(0, None, FAKE, 128, 7168, 256, None, FAKE, ws, None), -1)
-    err(L.moe_route_probe(0, FAKE, FAKE, 128, 7168, 256, None, FAKE, ws - 1, None), -4)
-    err(L.moe_route_probe(0, FAKE, FAKE, 128, 7168, 256, None, None, ws, None), -4)
-    err(L.moe_route_probe(0, ctypes.c_void_p(0x10008), FAKE, 128, 7168, 256, None, FAKE, ws,
-                          None), -6)
-
-
 def test_route_permute_workspace_and_validation():
     """moe_route_permute: workspace = the route's (rounded up to 256 bytes)
     then the permute's with its fp8 scale stage (T * H/128 fp32, rounded up
