@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void combine_wave_kernel(const u32x4* __restri
 #pragma unroll
         for (int e = 0; e < NE; ++e) acc[e] += wj * f[e];
       }
-      st_nt(out + i0 + q * 64 + lane, VT::pack(acc));
+      st_sc1(out + i0 + q * 64 + lane, VT::pack(acc));
     }
   }
 }

@@ -31,6 +31,15 @@ __device__ __forceinline__ unsigned int pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ u32x4 ld_nt(const u32x4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void st_nt(u32x4* p, u32x4 v) { __builtin_nontemporal_store(v, p); }
 
+// 16-byte global store with the gfx950 sc1 cache-policy bit (device scope)
+// and without nt; no compiler builtin sets it on a global store.  Used for
+// the combine's output rows: at the DeepSeek-V3 shape the C4 step took 1.658
+// against 1.680 ms with the nt store (same process, builds alternated, each
+// step after a 1 GiB rewrite), 1.640 against 1.662 ms back to back.
+__device__ __forceinline__ void st_sc1(u32x4* p, u32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
 }  // namespace moe
 
 // ---------------------------------------------------------------------------

@@ -3,23 +3,27 @@
 //
 // Replaces the reference's cublasGemmEx (K:4327-4339) followed by
 // topk_kernel (K:1829-1920), which writes the [T,E] fp32 logits to HBM and
-// reads them back.  Here a workgroup owns 128 tokens x all 256 experts:
+// reads them back.  Here a workgroup owns BM tokens x all E experts (128 x 256
+// at the DeepSeek-V3 shape, 64 x 128 at Qwen3-MoE's):
 //
-//   weights     a small pre-pass copies w[256, H] into a fragment-major
+//   weights     a small pre-pass copies w[E, H] into a fragment-major
 //               layout, so every MFMA B fragment a wave loads is 1 KB
-//               contiguous (the row-major rows are 14 KB apart and land on
-//               few L2 channels: the weight stream ran at ~2/3 of the speed).
-//   main loop   x[128, 64-wide K step] is brought into an LDS ring by the
-//               gfx950 global_load_lds DMA, D = 4 steps ahead.  Each of the
-//               8 waves (two per SIMD: one wave alone cannot issue MFMAs at
-//               the matrix core's rate) owns 32 experts, so its weight slice
-//               is private and goes straight to registers, also D steps
-//               ahead.  v_mfma_f32_16x16x32_bf16, fp32 accumulate, K in the
-//               same order as the standalone GEMM (identical logits).  x and
-//               w loads share the in-order vmcnt counter: waiting for a
-//               step's weights retires its x stage too, and a wave never has
-//               more than 63 loads in flight (the counter's limit).
-//   epilogue    the 128 x 256 fp32 tile goes through LDS once; its rows are
+//               contiguous (read row-major, the 14 KB-strided rows of one K
+//               step land on few L2 channels).
+//   main loop   x comes into an LDS ring by the gfx950 buffer_load ... lds
+//               DMA, one stage = two 64-wide K steps (256 contiguous bytes of
+//               every row), NSTG - 1 stages ahead.  Each of the 8 waves (two
+//               per SIMD) owns E/8 experts, so its weight slice is private and
+//               goes straight to registers, DW steps ahead.
+//               v_mfma_f32_16x16x32_bf16, fp32 accumulate, K in order (the
+//               logits equal the standalone GEMM's bit for bit).  x and w
+//               loads share the in-order vmcnt counter, so the wave's program
+//               order of loads is replayed at compile time (rf::Sched) and
+//               every wait names exactly the loads the step needs; a wait for
+//               a step's weights also retires every x stage issued before
+//               them, so the weights' depth DW is the x stream's latency
+//               budget too.  Rows past T read as zeros (buffer bounds).
+//   epilogue    the BM x E fp32 tile goes through LDS once; its rows are
 //               copied out to router_logits (1 KB per wavefront store,
 //               non-temporal), then 8 lanes per token (16 at E = 128) score
 //               it with the scoring kernel's per-token routine (bit-identical
@@ -27,207 +31,270 @@
 //               expert histogram -- optionally one per 256 (token,
 //               slot) pairs, the permute's block histograms, so the permute
 //               needs no histogram pass.
+#include <utility>
+
 #include "moe_common.h"
 #include "score_token.h"
 
 namespace moe {
 
 namespace rf {
-constexpr int BK = 64, ROWB = BK * 2, CH = 8;
-__device__ __forceinline__ int swz(int r) { return (r >> 1) & (CH - 1); }
-// BM tokens x E experts per workgroup: the x ring stage (BM rows of one 64-wide
-// K step) and the epilogue's fp32 tile (row stride E + 4 floats)
-constexpr int stage_bytes(int BM) { return BM * ROWB; }
-constexpr int tile_ld(int E) { return E + 4; }
-constexpr int tile_bytes(int BM, int E) { return BM * tile_ld(E) * 4; }
-}  // namespace rf
+constexpr int BK = 64;
+// word 3 of a gfx9 raw buffer resource (32-bit data format, no swizzle)
+constexpr int kRsrcW3 = 0x00020000;
 
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
 // bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima).
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-// N (8 or 4) 16-byte LDS reads 2 KB apart, issued as one instruction group
-// the compiler does not track (early-clobber outputs: no output may share the
-// address register); the caller places the lgkmcnt wait (an asm that takes
-// the registers as "+v" operands, so nothing reads them before it).
-template <int N>
+// One wave's vector-memory loads in program order.  Prologue: x stages
+// 0 .. DX-1 (NX loads each), then the weights of steps 0 .. DW-1 (NW each).
+// Step p: [at a stage start: wait, barrier, x stage p/SPS + DX] wait for the
+// step's weights; MFMAs; weights of step p + DW.  wait_at(p) is the vmcnt
+// that retires exactly the loads step p needs (its weights and, at a stage
+// start, its x stage); loads complete in issue order.
+struct Sched {
+  int SPS, DX, DW, NX, NW;
+  constexpr int issued_before_step(int p) const {
+    return DX * NX + DW * NW + ((p + SPS - 1) / SPS) * NX + p * NW;
+  }
+  constexpr int pos_x(int st) const {  // loads up to and including x stage st
+    if (st < DX) return (st + 1) * NX;
+    return issued_before_step((st - DX) * SPS) + NX;
+  }
+  constexpr int pos_w(int p) const {  // ... including the weights of step p
+    if (p < DW) return DX * NX + (p + 1) * NW;
+    const int q = p - DW;
+    return issued_before_step(q) + ((q % SPS) == 0 ? NX : 0) + NW;
+  }
+  constexpr int wait_at(int p) const {
+    int need = pos_w(p);
+    if (p % SPS == 0) {
+      const int px = pos_x(p / SPS);
+      need = need > px ? need : px;
+    }
+    return issued_before_step(p) - need;
+  }
+};
+
+// The kernel's shape: BM tokens x E experts, H = 64 * KT, 8 waves.
+template <int BM, int E, int KT>
+struct Cfg {
+  static constexpr int NWV = 8, NT = 64 * NWV;
+  static constexpr int SPS = 2;                     // K steps per x stage
+  static constexpr int NSTG = E == 256 ? 4 : 8;     // x ring stages
+  static constexpr int DW = E == 256 ? 5 : 6;       // weight steps in flight
+  static constexpr int ROWB = SPS * BK * 2;         // LDS row pitch of a stage
+  static constexpr int STAGE_B = BM * ROWB;
+  static constexpr int DX = NSTG - 1, NST = KT / SPS;
+  static constexpr int WE = E / NWV, NJ = WE / 16, NW = 2 * NJ, FM = BM / 16;
+  static constexpr int NX = STAGE_B / 1024 / NWV;   // 1 KB DMA instructions per wave per stage
+  static constexpr int TILE_LD = E + 4;             // epilogue tile row stride (floats)
+  static constexpr int LDSB = NSTG * STAGE_B > BM * TILE_LD * 4 ? NSTG * STAGE_B : BM * TILE_LD * 4;
+  static constexpr Sched S{SPS, DX, DW, NX, NW};
+  static_assert(KT % SPS == 0 && NX >= 1 && NJ >= 1 && (FM == 8 || FM == 4), "tile shape");
+  static_assert(DX * NX + DW * NW <= 63, "vmcnt range");
+};
+
+// 16-byte chunk c of stage row r -> its LDS slot: the 16 rows of one fragment
+// read land in 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int xslot(int r, int c) { return c ^ (r & 15); }
+}  // namespace rf
+
+// N (8 or 4) 16-byte LDS reads 16 rows apart (row pitch RB bytes), issued as
+// one instruction group the compiler does not track (early-clobber outputs:
+// no output may share the address register); lds_wait places the wait.
+template <int N, int RB>
 __device__ __forceinline__ void lds_readn(bf16x8 (&d)[N], unsigned ad) {
   static_assert(N == 8 || N == 4, "fragment count");
   if constexpr (N == 8)
     asm volatile(
-        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:2048\n\t"
-        "ds_read_b128 %2, %8 offset:4096\n\tds_read_b128 %3, %8 offset:6144\n\t"
-        "ds_read_b128 %4, %8 offset:8192\n\tds_read_b128 %5, %8 offset:10240\n\t"
-        "ds_read_b128 %6, %8 offset:12288\n\tds_read_b128 %7, %8 offset:14336"
+        "ds_read_b128 %0, %8\n\tds_read_b128 %1, %8 offset:%9\n\t"
+        "ds_read_b128 %2, %8 offset:%10\n\tds_read_b128 %3, %8 offset:%11\n\t"
+        "ds_read_b128 %4, %8 offset:%12\n\tds_read_b128 %5, %8 offset:%13\n\t"
+        "ds_read_b128 %6, %8 offset:%14\n\tds_read_b128 %7, %8 offset:%15"
         : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3]), "=&v"(d[4]), "=&v"(d[5]),
           "=&v"(d[6]), "=&v"(d[7])
-        : "v"(ad)
+        : "v"(ad), "n"(16 * RB), "n"(32 * RB), "n"(48 * RB), "n"(64 * RB), "n"(80 * RB),
+          "n"(96 * RB), "n"(112 * RB)
         : "memory");
   else
     asm volatile(
-        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:2048\n\t"
-        "ds_read_b128 %2, %4 offset:4096\n\tds_read_b128 %3, %4 offset:6144"
+        "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:%5\n\t"
+        "ds_read_b128 %2, %4 offset:%6\n\tds_read_b128 %3, %4 offset:%7"
         : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3])
-        : "v"(ad)
+        : "v"(ad), "n"(16 * RB), "n"(32 * RB), "n"(48 * RB)
         : "memory");
 }
 
-// wait for every outstanding LDS read; the N registers pass through the asm
-template <int N>
+// wait for the LDS reads: all but the last CNT issued; the N registers pass
+// through the asm, so nothing reads them before it
+template <int CNT, int N>
 __device__ __forceinline__ void lds_wait(bf16x8 (&d)[N]) {
   if constexpr (N == 8)
-    asm volatile("s_waitcnt lgkmcnt(0)"
+    asm volatile("s_waitcnt lgkmcnt(%8)"
                  : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(d[4]), "+v"(d[5]),
-                   "+v"(d[6]), "+v"(d[7])::"memory");
+                   "+v"(d[6]), "+v"(d[7])
+                 : "n"(CNT)
+                 : "memory");
   else
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3])::"memory");
+    asm volatile("s_waitcnt lgkmcnt(%4)"
+                 : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3])
+                 : "n"(CNT)
+                 : "memory");
 }
 
-// Bytes of LDS the kernel needs: the x ring or the epilogue tile.
-constexpr int route_fused_lds(int BM, int E, int D) {
-  return (D + 1) * rf::stage_bytes(BM) > rf::tile_bytes(BM, E) ? (D + 1) * rf::stage_bytes(BM)
-                                                                 : rf::tile_bytes(BM, E);
+// x DMA of one 16-byte piece per lane into LDS (buffer_load_dwordx4 ... lds);
+// NT: non-temporal (aux bit 1), so the line is not kept in the memory-side cache
+template <bool NT>
+__device__ __forceinline__ void rf_dma16(__amdgpu_buffer_rsrc_t r, char* l, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)l, 16,
+                                           voff, soff, 0, NT ? 2 : 0);
 }
 
-// BM tokens (128 or 64) x E experts (256 or 128) per workgroup.  NWV waves
-// (64 * NWV threads, NWV / 4 per SIMD): wave w owns experts [w*WE, (w+1)*WE)
-// of all BM rows, so its weight slice is its own and goes straight to
-// registers; x is shared through the LDS ring.  D: K steps of loads in
-// flight.  KTC: the K steps, fully unrolled.  V, KK, SC: the scoring lane
-// width, k (0: runtime) and rule.  NTOK: tokens one lane group scores per pass.
-// nt_from: the first tile whose x loads are non-temporal (rf_temporal_tiles).
-template <int BM, int E, int NWV, int D, int KTC, int V, int KK, int SC, int NTOK>
-__global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
+// The K loop of one BM-token tile: acc[i][j] = the wave's 16 x 16 blocks
+// (rows i*16.., experts wave*WE + j*16..), fp32.  NTX: x loads non-temporal.
+// The whole loop is unrolled (one instantiation per step), so every ring slot,
+// register slot and wait count is a constant.
+template <int BM, int E, int KT, bool NTX>
+__device__ __forceinline__ void rf_kloop(const __bf16* __restrict__ x,
+                                         const __bf16* __restrict__ wf, int T, char* lds,
+                                         f32x4 (&acc)[BM / 16][E / 128]) {
+  using C = rf::Cfg<BM, E, KT>;
+  using namespace rf;
+  constexpr int H = KT * BK, ROWB = C::ROWB, STAGE_B = C::STAGE_B, NSTG = C::NSTG;
+  constexpr int NJ = C::NJ, NW = C::NW, DX = C::DX, DW = C::DW, NX = C::NX, FM = C::FM;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const long long m0 = (long long)blockIdx.x * BM;
+  const int fr = lane & 15, fc = lane >> 4;
+  const int rows = T - m0 < BM ? (int)(T - m0) : BM;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(x + m0 * H), (short)0, rows * H * 2, kRsrcW3);
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)wf, (short)0, E * H * 2, kRsrcW3);
+
+  // x DMA: instruction q of this wave covers stage rows (wave*NX + q)*RPI ..;
+  // lane l writes the 16 bytes at LDS offset l*16 of the instruction's 1 KB
+  constexpr int RPI = 1024 / ROWB, CPR = ROWB / 16;
+  int voff_x[NX];
+#pragma unroll
+  for (int q = 0; q < NX; ++q) {
+    const int r = (wave * NX + q) * RPI + lane / CPR, p = lane % CPR;
+    voff_x[q] = r * H * 2 + xslot(r, p) * 16;
+  }
+  auto issue_x = [&](int st) {
+    const int ls = st < C::NST ? st : C::NST - 1;  // past the end: reload the last stage
+#pragma unroll
+    for (int q = 0; q < NX; ++q)
+      rf_dma16<NTX>(rx, lds + (st % NSTG) * STAGE_B + (wave * NX + q) * 1024, voff_x[q],
+                    ls * ROWB);
+  };
+  // weights: fragment (kt*2 + kk)*(E/16) + wave*NJ + j, 1 KB each
+  const int voff_w = (wave * NJ * 64 + lane) * 16;
+  bf16x8 wr[DW][NW];
+  auto issue_w = [&](int p, bf16x8 (&dst)[NW]) {
+    if (p >= KT) p = KT - 1;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        dst[kk * NJ + j] = __builtin_bit_cast(
+            bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rw, voff_w + j * 1024,
+                                                          (p * 2 + kk) * E * 64, 0));
+  };
+
+#pragma unroll
+  for (int st = 0; st < DX; ++st) issue_x(st);
+#pragma unroll
+  for (int p = 0; p < DW; ++p) issue_w(p, wr[p]);
+  const unsigned fbase =
+      (unsigned)(uintptr_t)(__attribute__((address_space(3))) const char*)lds + fr * ROWB;
+  bf16x8 a[FM];
+  auto step = [&]<int P>(std::integral_constant<int, P>) __attribute__((always_inline)) {
+    constexpr int VM = C::S.wait_at(P);
+    static_assert(VM >= 0 && VM <= 63, "vmcnt");
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(VM));
+    if constexpr (P % C::SPS == 0) {
+      // every wave's part of this stage has landed and every wave is done
+      // with the previous stage's slot, which the new DMA refills
+      __builtin_amdgcn_s_barrier();
+      issue_x(P / C::SPS + DX);
+    }
+    constexpr int slot = (P / C::SPS) % NSTG;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const unsigned ad =
+          fbase + slot * STAGE_B + xslot(fr, (P % C::SPS) * 8 + kk * 4 + fc) * 16;
+      if constexpr (FM == 8) {
+        // two groups of four fragments: the first group's MFMAs start while
+        // the second group's reads are in flight
+        bf16x8(&lo)[4] = *reinterpret_cast<bf16x8(*)[4]>(&a[0]);
+        bf16x8(&hi)[4] = *reinterpret_cast<bf16x8(*)[4]>(&a[4]);
+        lds_readn<4, ROWB>(lo, ad);
+        lds_readn<4, ROWB>(hi, ad + 64 * ROWB);
+        lds_wait<4>(lo);
+      } else {
+        lds_readn<FM, ROWB>(a, ad);
+        lds_wait<0>(a);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if constexpr (FM == 8) {
+          if (i == 4) {
+            __builtin_amdgcn_sched_barrier(0);
+            lds_wait<0>(*reinterpret_cast<bf16x8(*)[4]>(&a[4]));
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], wr[P % DW][kk * NJ + j],
+                                                              acc[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    issue_w(P + DW, wr[P % DW]);
+  };
+  [&]<int... Ps>(std::integer_sequence<int, Ps...>) __attribute__((always_inline)) {
+    (step(std::integral_constant<int, Ps>{}), ...);
+  }(std::make_integer_sequence<int, KT>{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// BM tokens (128 or 64) x E experts (256 or 128) per workgroup, 8 waves: wave
+// w owns experts [w*E/8, (w+1)*E/8) of all BM rows.  KT: the K steps.  V, KK,
+// SC: the scoring lane width, k (0: runtime) and rule.  nt_from: the first
+// tile whose x loads are non-temporal (rf_temporal_tiles).
+template <int BM, int E, int KT, int V, int KK, int SC>
+__global__ __launch_bounds__(512, 1) void route_fused_kernel(
     const __bf16* __restrict__ x, const __bf16* __restrict__ wf, const float* __restrict__ bias,
     int T, int H, int k_rt, int renorm, int n_group, int topk_group, float route_scale,
     float norm_min, float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ wout,
     int* __restrict__ counts, int* __restrict__ blockcnt, int nblk, int pt_log2,
     int nt_from) {
-  using namespace rf;
-  constexpr int NT = 64 * NWV;             // threads
-  constexpr int FM = BM / 16;              // 16-row fragments per K half
-  constexpr int STAGE_B = stage_bytes(BM);
-  constexpr int TILE_LD = tile_ld(E);
-  constexpr int WE = E / NWV;              // experts per wave
-  constexpr int NJ = WE / 16;              // 16-expert fragment columns per wave
-  constexpr int NX = (BM / 8) / NWV;       // x DMA instructions per wave per stage
-  constexpr int NWF = 2 * NJ;              // weight fragments per wave per step (two K halves)
-  constexpr int NS = D + 1;                // x ring stages
-  // every wave keeps at most 63 vector loads in flight (the vmcnt limit: the
-  // counter does not account for more)
-  static_assert(D * (NX + NWF) <= 63, "too many loads in flight per wave");
-  static_assert(NX >= 1 && NJ >= 1, "tile shape");
-  __shared__ __attribute__((aligned(1024))) char lds[route_fused_lds(BM, E, D)];
-
+  using C = rf::Cfg<BM, E, KT>;
+  constexpr int NT = C::NT, FM = C::FM, NJ = C::NJ, WE = C::WE, TILE_LD = C::TILE_LD;
+  constexpr int NTOK = E == 256 ? 2 : 1;  // tokens a lane group scores per pass
+  __shared__ __attribute__((aligned(1024))) char lds[C::LDSB];
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wg = wave;                     // expert group
+  const int wg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // expert group
   const long long m0 = (long long)blockIdx.x * BM;
-  const int KT = KTC > 0 ? KTC : H / BK;
   const int fr = lane & 15, fc = lane >> 4;
-
-  // x DMA sources (rows past T clamped: loaded, never stored)
-  const __bf16* xsrc[NX];
-#pragma unroll
-  for (int q = 0; q < NX; ++q) {
-    const int gi = wave * NX + q;
-    const int r = gi * 8 + lane / 8, p = lane % 8;
-    long long row = m0 + r;
-    if (row >= T) row = T - 1;
-    xsrc[q] = x + row * H + (p ^ swz(r)) * 8;
-  }
-
-  // x step `src_kt` into the ring slot of step `kt`
-  auto issue_x = [&](int kt, int src_kt) {
-    char* st = lds + (kt % NS) * STAGE_B;
-#pragma unroll
-    for (int q = 0; q < NX; ++q) {
-      auto* dst = (__attribute__((address_space(3))) void*)(st + (wave * NX + q) * 1024);
-      // tiles from nt_from on: non-temporal (aux bit 1: nt), so they do not
-      // displace the rows of the earlier tiles from the memory-side cache
-      const int sk = src_kt;
-      if ((int)blockIdx.x >= nt_from)
-        __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + sk * BK), dst, 16, 0, 2);
-      else
-        __builtin_amdgcn_global_load_lds((const void*)(xsrc[q] + sk * BK), dst, 16, 0, 0);
-    }
-  };
-  bf16x8 wr[D][NWF];
-  auto issue_w = [&](int kt, bf16x8 (&dst)[NWF]) {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        dst[kk * NJ + j] = *reinterpret_cast<const bf16x8*>(
-            wf + ((long long)((kt * 2 + kk) * (E / 16) + wg * NJ + j) * 64 + lane) * 8);
-  };
-  constexpr int VMW = (D - 1) * (NX + NWF);
 
   f32x4 acc[FM][NJ];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  if ((int)blockIdx.x >= nt_from)
+    rf_kloop<BM, E, KT, true>(x, wf, T, lds, acc);
+  else
+    rf_kloop<BM, E, KT, false>(x, wf, T, lds, acc);
 
-  // prologue: steps 0 .. D-1 in flight (KT % D == 0 is required by the launcher)
-#pragma unroll
-  for (int u = 0; u < D; ++u) {
-    issue_x(u, u);
-    issue_w(u, wr[u]);
-  }
-
-  // Every step waits, computes and refills the same way: the last D steps
-  // reload step KT-1 into slots nobody reads again, so the compiler sees one
-  // uniform sequence and the vmcnt count below holds on every step.
-  bf16x8 a0[FM], a1[FM];
-#pragma unroll
-  for (int kb = 0; kb < KT; kb += D) {
-#pragma unroll
-    for (int u = 0; u < D; ++u) {
-      const int kt = kb + u;
-      // stage kt and weights kt are the oldest loads once at most (D-1)
-      // later steps' loads are pending.  The wait is the builtin, not asm,
-      // so the compiler's own vmcnt bookkeeping knows they are retired.
-      __builtin_amdgcn_s_waitcnt(vmcnt_only(VMW));
-      __builtin_amdgcn_s_barrier();
-      const char* sb = lds + (kt % NS) * STAGE_B;
-      // refill x first: stage kt + D goes to the slot of stage kt - 1, which
-      // every wave finished reading before this step's barrier, so its DMA can
-      // start before this step's fragment reads and MFMAs
-      const int kn = kt + D < KT ? kt + D : KT - 1;
-      issue_x(kt + D, kn);
-      // rows i*16 + fr share the swizzle of fr: a half step's FM fragment
-      // reads are 2 KB apart
-      auto frag_addr = [&](int kk) {
-        return (unsigned)(uintptr_t)((__attribute__((address_space(3))) const char*)(
-            sb + fr * ROWB + (((kk * 4 + fc) ^ swz(fr)) * 16)));
-      };
-      lds_readn<FM>(a0, frag_addr(0));
-      lds_wait<FM>(a0);
-      // the second half's reads go out before the first half's MFMAs and
-      // land while they run
-      lds_readn<FM>(a1, frag_addr(1));
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0[i], wr[u][j], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      lds_wait<FM>(a1);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] =
-              __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], wr[u][NJ + j], acc[i][j], 0, 0, 0);
-      // refill the weights of step kt + D once this step's MFMAs have read them
-      issue_w(kn, wr[u]);
-    }
-  }
-
-  // ---- epilogue: the fp32 tile through LDS
-  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  // ---- epilogue: the fp32 tile through LDS (over the ring: every wave is
+  // past its last fragment read once it reaches this barrier)
+  __syncthreads();
   float* tile = reinterpret_cast<float*>(lds);
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -269,8 +336,11 @@ __global__ __launch_bounds__(64 * NWV, 1) void route_fused_kernel(
 #pragma unroll
   for (int j = 0; j < V; ++j) bl[j] = bias ? bias[e0 + j] : 0.0f;
   const int k = KK > 0 ? KK : k_rt;
-  // each G-lane group scores NTOK tokens per pass (tl, tl + TPP, ...); two or
-  // four interleaved tokens measured no faster than one (175-180 us per call)
+  // each G-lane group scores NTOK tokens per pass (tl, tl + TPP, ...): every
+  // tile finishes its K loop at about the same time, so the scoring is not
+  // hidden behind other tiles' loops, and two interleaved tokens hide the
+  // latency of its cross-lane chains (C4 route stage 150 -> 145 us with
+  // every x load non-temporal)
   static_assert(BM % (TPP * NTOK) == 0, "token passes");
   for (int tl0 = threadIdx.x / G; tl0 < BM; tl0 += TPP * NTOK) {
     float l[NTOK][V];
@@ -344,15 +414,13 @@ __global__ void rf_zero_kernel(int* __restrict__ p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// The configurations shipped: 8 waves (two per SIMD; one wave per SIMD issues
-// MFMAs at about a third of the rate), loads D = 4 steps ahead, one token per
-// lane group per scoring pass, the K loop fully unrolled (a runtime trip count
-// makes the compiler merge its load bookkeeping at the loop head into a
-// vmcnt(0) that drains every load in flight once per iteration):
-//   E = 256, H = 7168 (DeepSeek-V3): 128-token tiles, 112 K steps;
+// The configurations shipped (rf::Cfg): 8 waves (two per SIMD), one token per
+// lane group per scoring pass, the K loop fully unrolled:
+//   E = 256, H = 7168 (DeepSeek-V3): 128-token tiles, 112 K steps, 4 x-ring
+//                                    stages of 32 KB, weights 5 steps ahead;
 //   E = 128, H = 2048 (Qwen3-MoE):   64-token tiles (256 of them at T = 16384),
-//                                    32 K steps.
-constexpr int kRfWaves = 8, kRfDepth = 4, kRfScoreTokens = 1;
+//                                    32 K steps, 8 stages of 16 KB, weights 6
+//                                    steps ahead.
 
 // Experts per scoring lane: 32 at E = 256 (8 lanes per token; a DeepSeek-V3
 // group of 32 is one lane, so its top-2 needs no lane exchange: 4-6 us less
@@ -386,12 +454,12 @@ size_t route_fused_workspace_bytes(int E, int H) { return (size_t)E * H * 2; }
 // Instead, the tiles of the first kRfMallBytes of x (in token order) load
 // temporal and the rest non-temporal, so the MALL keeps whole rows of the
 // tokens the gather reads first; the logits go out non-temporal, so they take
-// none of it.  Measured at the DeepSeek-V3 shape (C4 step, 5 runs of 20 steps
-// each, 128-token tiles): all temporal 1.700 ms, all non-temporal 1.709; with
-// the logits stored temporal from registers, the first 100 / 109 / 120 tiles
-// temporal 1.681 / 1.678 / 1.685; with the non-temporal row copy of the
-// logits, 109 / 120 / 130 / 140 / 150 / 160 tiles 1.675 / 1.675 / 1.669 /
-// 1.672 / 1.685 / 1.695.
+// none of it.  A temporal load that finds the MALL full of dirty lines (the
+// previous step's output, a cache flush) pays for their write-back: the
+// temporal tiles' K loops run ~25 us longer than the non-temporal ones, and
+// the gather gains ~45 us.  Measured at the DeepSeek-V3 shape (C4 step,
+// builds alternated in one session, each step after a 1 GiB rewrite): 0 /
+// 114 / 228 / 280 MiB temporal 1.719 / 1.700 / 1.686 / 1.706 ms.
 constexpr long long kRfMallBytes = 228ll << 20;
 static int rf_temporal_tiles(int BM, int H) {
   const long long t = kRfMallBytes / ((long long)BM * H * 2);
@@ -403,7 +471,7 @@ static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias
                             int k, int renorm, int n_group, int topk_group, float route_scale,
                             float norm_min, float* logits, int32_t* ids, float* wout,
                             int32_t* counts, int32_t* blockcnt, hipStream_t s) {
-  auto kern = route_fused_kernel<BM, E, kRfWaves, kRfDepth, KTC, V, KK, SC, kRfScoreTokens>;
+  auto kern = route_fused_kernel<BM, E, KTC, V, KK, SC>;
   // blocks of 256 pairs = 2^pt_log2 tokens (k a power of two), else one
   // histogram per tile
   int pt_log2 = 31;
@@ -412,7 +480,7 @@ static hipError_t launch_rf(const __bf16* x, const __bf16* wf, const float* bias
     while ((k << pt_log2) < kPairsPerBlock) ++pt_log2;
   }
   const int nblk = dispatch_blocks((long long)T * k);
-  hipLaunchKernelGGL(kern, dim3((unsigned)((T + BM - 1) / BM)), dim3(64 * kRfWaves), 0, s, x, wf,
+  hipLaunchKernelGGL(kern, dim3((unsigned)((T + BM - 1) / BM)), dim3(rf::Cfg<BM, E, KTC>::NT), 0, s, x, wf,
                      bias, T, H, k, renorm, n_group, topk_group, route_scale, norm_min, logits,
                      ids, wout, counts, blockcnt, nblk, pt_log2, rf_temporal_tiles(BM, H));
   return hipGetLastError();

@@ -26,7 +26,7 @@ EXAMPLE_SRC = os.path.join(PKG_ROOT, "examples", "moe_step.cpp")
 EXAMPLE_BIN = os.path.join(HERE, "moe_step")
 
 FLAGS = [
-    "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-O3", "-std=c++20", "-fPIC", "-shared",
     "--offload-arch=gfx950",
     # packed fp32 VALU ops are kept out of every device function
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

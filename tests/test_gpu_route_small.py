@@ -123,11 +123,12 @@ def test_route_small_repeat(cuda):
 def test_route_small_fp32_weights(cuda, H, T, k):
     """E = 8 with an fp32 weight (C1's toy route): the kernel loads the fp32
     rows and splits them hi = bf16(w), lo = bf16(w - hi) as its 16 fragment
-    columns, and each logit is the sum of eight partials, hi then lo per K
-    quarter -- equal, bit for bit, to the standalone GEMM over each quarter of
-    each half (split here on the host side of the comparison) added in that
-    order; selection equals the scoring kernel's and the oracle's; no
-    workspace."""
+    columns, and each logit is (sum of the four hi partials) + (sum of the
+    four lo partials), each in K-quarter order (the reference's fold of the
+    whole hi and lo products) -- equal, bit for bit, to the standalone GEMM
+    over each quarter of each half (split here on the host side of the
+    comparison) added that way; selection equals the scoring kernel's and the
+    oracle's; no workspace."""
     print("route_small fp32 H=%d T=%d k=%d" % (H, T, k), flush=True)
     E = 8
     cfg = CFGS["softmax"]
@@ -140,18 +141,21 @@ def test_route_small_fp32_weights(cuda, H, T, k):
     hi = w.bfloat16()
     lo = (w - hi.float()).bfloat16()
     kw = H // 4
-    acc = None
-    for q in range(4):
-        xq = x[:, q * kw:(q + 1) * kw].contiguous()
-        for half in (hi, lo):
+    sums = []
+    for half in (hi, lo):
+        acc = None
+        for q in range(4):
+            xq = x[:, q * kw:(q + 1) * kw].contiguous()
             wq = half[:, q * kw:(q + 1) * kw].contiguous()
             p = torch.empty(T, E, dtype=torch.float32, device=cuda)
             rc = L.moe_router_gemm(M._ptr(xq), M._ptr(wq), T, kw, E, M._ptr(p), M._stream(x))
             assert rc == 0, L.moe_last_error_string()
             acc = p if acc is None else acc + p
+        sums.append(acc)
+    acc = sums[0] + sums[1]
     ido, wo, co = M.topk(lf, None, k, cfg)
     torch.cuda.synchronize()
-    assert torch.equal(lf, acc), "logits differ from the hi/lo K-quarter GEMMs added in order"
+    assert torch.equal(lf, acc), "logits differ from (sum of hi quarters) + (sum of lo quarters)"
     assert torch.equal(idf, ido) and torch.equal(wf, wo) and torch.equal(cf, co)
     ocfg = O.RouteCfg(cfg.scoring, cfg.renormalize, cfg.n_group, cfg.topk_group,
                       cfg.route_scale, cfg.norm_min)
