@@ -219,6 +219,13 @@ __global__ __launch_bounds__(kPairsPerBlock) void dispatch_index_kernel(
   int rank = __popcll(me[wv] & ((1ull << bit) - 1ull));
   for (int w = 0; w < wv; ++w) rank += __popcll(me[w]);
   const int pos = offs[e] + (SUM ? sbase[e] : blockbase[(long long)e * nblk + blockIdx.x]) + rank;
+  // histograms that do not match the ids (a caller's inconsistent buffers)
+  // give positions outside [0, npairs): the pair is dropped (pair_row -1, which
+  // the gather and the combine skip) instead of written out of bounds
+  if (pos < 0 || pos >= npairs) {
+    pair_row[p] = -1;
+    return;
+  }
   pair_row[p] = pos;
   row_token[pos] = (int)(p / k);
 }

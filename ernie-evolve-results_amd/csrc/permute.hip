@@ -155,7 +155,7 @@ template <int W>
 __global__ __launch_bounds__(256) void scatter_scales_kernel(const float* __restrict__ stage,
                                                              const int* __restrict__ row_token,
                                                              const int* __restrict__ nrows_p,
-                                                             long long nitems, int nb,
+                                                             long long nitems, int nb, int T,
                                                              float* __restrict__ scales) {
   using Piece = typename std::conditional<W == 4, u32x4, float>::type;
   const int per_row = nb / W;
@@ -172,8 +172,10 @@ __global__ __launch_bounds__(256) void scatter_scales_kernel(const float* __rest
     if (q < nitems && r < nrows) {
       const int p = (int)(q - r * per_row);
       const long long t = row_token[r];
-      v[i] = reinterpret_cast<const Piece*>(stage + t * nb)[p];
-      dst[i] = r * per_row + p;
+      if (t >= 0 && t < T) {  // a row the index pass dropped holds no token
+        v[i] = reinterpret_cast<const Piece*>(stage + t * nb)[p];
+        dst[i] = r * per_row + p;
+      }
     }
   }
 #pragma unroll
@@ -202,10 +204,10 @@ hipError_t launch_gather_fp8(const void* x, const int32_t* pair_row, const int32
   const dim3 sgrid((unsigned)((nitems + 256LL * kScatterItems - 1) / (256LL * kScatterItems)));
   if (vec)
     hipLaunchKernelGGL(scatter_scales_kernel<4>, sgrid, dim3(256), 0, s, stage, row_token, nrows,
-                       nitems, nb, scales);
+                       nitems, nb, T, scales);
   else
     hipLaunchKernelGGL(scatter_scales_kernel<1>, sgrid, dim3(256), 0, s, stage, row_token, nrows,
-                       nitems, nb, scales);
+                       nitems, nb, T, scales);
   return hipGetLastError();
 }
 
