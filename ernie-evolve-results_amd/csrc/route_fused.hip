@@ -17,12 +17,11 @@
 //               goes straight to registers, DW steps ahead.
 //               v_mfma_f32_16x16x32_bf16, fp32 accumulate, K in order (the
 //               logits equal the standalone GEMM's bit for bit).  x and w
-//               loads share the in-order vmcnt counter, so the wave's program
-//               order of loads is replayed at compile time (rf::Sched) and
-//               every wait names exactly the loads the step needs; a wait for
-//               a step's weights also retires every x stage issued before
-//               them, so the weights' depth DW is the x stream's latency
-//               budget too.  Rows past T read as zeros (buffer bounds).
+//               loads share the vmcnt counter; each step's one wait
+//               (rf::Sched) counts only loads issued after the ones it must
+//               retire that are of the same kind, so it holds whatever order
+//               the x DMA and the weight loads complete in relative to each
+//               other.  Rows past T read as zeros (buffer bounds).
 //   epilogue    the BM x E fp32 tile goes through LDS once; its rows are
 //               copied out to router_logits (1 KB per wavefront store,
 //               non-temporal), then 8 lanes per token (16 at E = 128) score
@@ -48,32 +47,23 @@ constexpr int kRsrcW3 = 0x00020000;
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 // One wave's vector-memory loads in program order.  Prologue: x stages
-// 0 .. DX-1 (NX loads each), then the weights of steps 0 .. DW-1 (NW each).
+// 0 .. DX-1 (NX DMA loads each), then the weights of steps 0 .. DW-1 (NW each).
 // Step p: [at a stage start: wait, barrier, x stage p/SPS + DX] wait for the
-// step's weights; MFMAs; weights of step p + DW.  wait_at(p) is the vmcnt
-// that retires exactly the loads step p needs (its weights and, at a stage
-// start, its x stage); loads complete in issue order.
+// step's weights; MFMAs; weights of step p + DW.  wait_at(p) is the vmcnt that
+// retires the loads step p needs (its weights and, at a stage start, its x
+// stage) assuming only that loads of one kind complete in issue order: the x
+// DMA loads (into LDS) and the weight loads (into registers) are not assumed
+// to complete in order with respect to each other.  With W(p) outstanding, the
+// (DW-1)*NW weight loads issued after it are outstanding too, so a count of at
+// most (DW-1)*NW retires W(p); likewise (DX-1)*NX for x stage p/SPS.  (A count
+// that relied on the two kinds completing in one order read stale LDS rows on
+// the first, cold call of a configuration whose x ran only as far ahead as its
+// weights.)
 struct Sched {
   int SPS, DX, DW, NX, NW;
-  constexpr int issued_before_step(int p) const {
-    return DX * NX + DW * NW + ((p + SPS - 1) / SPS) * NX + p * NW;
-  }
-  constexpr int pos_x(int st) const {  // loads up to and including x stage st
-    if (st < DX) return (st + 1) * NX;
-    return issued_before_step((st - DX) * SPS) + NX;
-  }
-  constexpr int pos_w(int p) const {  // ... including the weights of step p
-    if (p < DW) return DX * NX + (p + 1) * NW;
-    const int q = p - DW;
-    return issued_before_step(q) + ((q % SPS) == 0 ? NX : 0) + NW;
-  }
   constexpr int wait_at(int p) const {
-    int need = pos_w(p);
-    if (p % SPS == 0) {
-      const int px = pos_x(p / SPS);
-      need = need > px ? need : px;
-    }
-    return issued_before_step(p) - need;
+    const int w = (DW - 1) * NW, xs = (DX - 1) * NX;
+    return (p % SPS == 0 && xs < w) ? xs : w;
   }
 };
 
@@ -82,8 +72,8 @@ template <int BM, int E, int KT>
 struct Cfg {
   static constexpr int NWV = 8, NT = 64 * NWV;
   static constexpr int SPS = 2;                     // K steps per x stage
-  static constexpr int NSTG = E == 256 ? 4 : 8;     // x ring stages
-  static constexpr int DW = E == 256 ? 5 : 6;       // weight steps in flight
+  static constexpr int NSTG = E == 256 ? 4 : 3;     // x ring stages
+  static constexpr int DW = E == 256 ? 5 : 4;       // weight steps in flight
   static constexpr int ROWB = SPS * BK * 2;         // LDS row pitch of a stage
   static constexpr int STAGE_B = BM * ROWB;
   static constexpr int DX = NSTG - 1, NST = KT / SPS;
@@ -419,8 +409,10 @@ __global__ void rf_zero_kernel(int* __restrict__ p, int n) {
 //   E = 256, H = 7168 (DeepSeek-V3): 128-token tiles, 112 K steps, 4 x-ring
 //                                    stages of 32 KB, weights 5 steps ahead;
 //   E = 128, H = 2048 (Qwen3-MoE):   64-token tiles (256 of them at T = 16384),
-//                                    32 K steps, 8 stages of 16 KB, weights 6
-//                                    steps ahead.
+//                                    32 K steps, 3 stages of 16 KB, weights 4
+//                                    steps ahead (route 25.4 us after a
+//                                    combine, against 26.1-28.3 us for 4-8
+//                                    stages and weights 3-8 ahead).
 
 // Experts per scoring lane: 32 at E = 256 (8 lanes per token; a DeepSeek-V3
 // group of 32 is one lane, so its top-2 needs no lane exchange: 4-6 us less
