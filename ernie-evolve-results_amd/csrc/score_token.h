@@ -153,6 +153,7 @@ __device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const floa
   // ---- scores: sel (what is ranked) and aux (what the weight is made of)
   float sel[NT][V];
   float fullsum[NT];
+  bool kept_grp[NT];  // sigmoid rule: the lane's expert group survived the group selection
 #pragma unroll
   for (int n = 0; n < NT; ++n) fullsum[n] = 1.0f;
   if constexpr (SC == kScoreSoftmax) {
@@ -219,6 +220,8 @@ __device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const floa
     for (int n = 0; n < NT; ++n)
 #pragma unroll
       for (int j = 0; j < V; ++j) sel[n][j] = det_sigmoid(l[n][j]) + b[j];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) kept_grp[n] = false;
     if (n_group > 1) {
       const int lgl = ilog2c((E / n_group) / V);  // log2(lanes per group), V divides the group
       float t1[NT], t2[NT], gscore[NT];
@@ -270,6 +273,8 @@ __device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const floa
         for (int n = 0; n < NT; ++n) kept[n] = kept[n] | (bg[n] == g);
       }
 #pragma unroll
+      for (int n = 0; n < NT; ++n) kept_grp[n] = kept[n];
+#pragma unroll
       for (int n = 0; n < NT; ++n)
 #pragma unroll
         for (int j = 0; j < V; ++j) sel[n][j] = kept[n] ? sel[n][j] : NEG_INF;
@@ -288,8 +293,67 @@ __device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const floa
     m0[n] = 0.0f;
     acc[n] = 0.0f;
   }
+  // Compacted rounds (sigmoid rule, 8 lanes of 32 experts per token, one lane
+  // per expert group, at most 4 groups kept, two tokens per lane group): the
+  // kept groups of token 0 move to lanes 0-3 and those of token 1 to lanes
+  // 4-7 (ds_bpermute, in group order), so each lane ranks one group of one
+  // token and a round reduces over 4 lanes -- half the rounds' work.  The
+  // winners are the same: each round takes the best remaining kept entry
+  // under (value desc, index asc), and the entries of dropped groups were
+  // -inf, which never win while a kept entry remains (k <= 32).
+  bool compact = false;
+  if constexpr (SC == kScoreSigmoidGroup && NT == 2 && G == 8 && V == 32) {
+    compact = n_group == G && topk_group >= 1 && topk_group <= 4 && k <= 8;
+    if (compact) {
+      const int lane = (int)(threadIdx.x & 63);
+      const int gb = lane & ~7;  // the lane group's first lane in the wave
+      const unsigned long long kb0 = __ballot(kept_grp[0]), kb1 = __ballot(kept_grp[1]);
+      const int half = gl >> 2, c = gl & 3;
+      const unsigned m = (unsigned)(((half ? kb1 : kb0) >> gb) & 0xFFull);
+      // the c-th (from 0) set bit of m: drop the c lowest set bits
+      const unsigned m1 = m & (m - 1u), m2 = m1 & (m1 - 1u), m3 = m2 & (m2 - 1u);
+      const unsigned mc = c == 0 ? m : (c == 1 ? m1 : (c == 2 ? m2 : m3));
+      const bool has = mc != 0u;
+      const int src = has ? (int)__builtin_ctz(mc) : gl;
+      const int addr = (gb + src) * 4;
+      const int ce0 = src * V;  // the first expert of the group this lane ranks
+      float cs[V];
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float a = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(sel[0][j])));
+        const float d = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(sel[1][j])));
+        cs[j] = has ? (half ? d : a) : NEG_INF;
+      }
+#pragma unroll
+      for (int r = 0; r < (KK > 0 ? KK : 8); ++r) {
+        if (KK == 0 && r >= k) break;
+        float bv;
+        int bi;
+        local_argmax<V>(cs, ce0, bv, bi);
+        MOE_FOR_LEVELS(0, 2, {
+          const float ov = partner_f<L_>(bv);
+          const int oi = partner_i<L_>(bi);
+          const bool take = (ov > bv) | ((ov == bv) & (oi < bi));
+          bv = take ? ov : bv;
+          bi = take ? oi : bi;
+        })
+        // the other token's winner, from the mirrored half of the 8 lanes
+        const float xv = partner_f<2>(bv);
+        const int xi = partner_i<2>(bi);
+        const int i0 = half ? xi : bi, i1 = half ? bi : xi;
+        const float v0 = half ? xv : bv, v1 = half ? bv : xv;
+        my_id[0] = gl == r ? i0 : my_id[0];
+        my_id[1] = gl == r ? i1 : my_id[1];
+        my_sel[0] = gl == r ? v0 : my_sel[0];
+        my_sel[1] = gl == r ? v1 : my_sel[1];
+#pragma unroll
+        for (int j = 0; j < V; ++j) cs[j] = ce0 + j == bi ? NEG_INF : cs[j];
+      }
+    }
+  }
 #pragma unroll
   for (int r = 0; r < (KK > 0 ? KK : 8); ++r) {
+    if (compact) break;
     if (KK == 0 && r >= k) break;
     float bv[NT];
     int bi[NT];
