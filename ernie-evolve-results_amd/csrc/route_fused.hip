@@ -300,11 +300,23 @@ __global__ __launch_bounds__(512, 1) void route_fused_kernel(
   // (a wavefront writes 1 KB of consecutive floats), non-temporal so they do
   // not take memory-side cache space from x; issued before the scoring, which
   // runs while they drain
-  for (int idx = threadIdx.x; idx < BM * (E / 4); idx += NT) {
-    const int row = idx / (E / 4), c4 = idx - row * (E / 4);
-    if (m0 + row < T)
-      __builtin_nontemporal_store(*reinterpret_cast<const f32x4*>(tile + row * TILE_LD + c4 * 4),
-                                  reinterpret_cast<f32x4*>(logits + (m0 + row) * E + c4 * 4));
+  {
+    constexpr int NCP = BM * (E / 4) / NT;  // 16-byte pieces per thread, all read before any store
+    static_assert(BM * (E / 4) % NT == 0, "logits copy");
+    f32x4 piece[NCP];
+#pragma unroll
+    for (int i = 0; i < NCP; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      const int row = idx / (E / 4), c4 = idx - row * (E / 4);
+      piece[i] = *reinterpret_cast<const f32x4*>(tile + row * TILE_LD + c4 * 4);
+    }
+#pragma unroll
+    for (int i = 0; i < NCP; ++i) {
+      const int idx = threadIdx.x + i * NT;
+      const int row = idx / (E / 4), c4 = idx - row * (E / 4);
+      if (m0 + row < T)
+        __builtin_nontemporal_store(piece[i], reinterpret_cast<f32x4*>(logits + (m0 + row) * E + c4 * 4));
+    }
   }
 
   // ---- scoring: G = E/V lanes per token
@@ -323,8 +335,12 @@ __global__ __launch_bounds__(512, 1) void route_fused_kernel(
   const int gl = threadIdx.x % G;
   const int e0 = gl * V;
   float bl[V];
+  if (bias) {
+    load_vec<V>(bias + e0, bl);
+  } else {
 #pragma unroll
-  for (int j = 0; j < V; ++j) bl[j] = bias ? bias[e0 + j] : 0.0f;
+    for (int j = 0; j < V; ++j) bl[j] = 0.0f;
+  }
   const int k = KK > 0 ? KK : k_rt;
   // each G-lane group scores NTOK tokens per pass (tl, tl + TPP, ...): every
   // tile finishes its K loop at about the same time, so the scoring is not

@@ -75,6 +75,32 @@ __device__ __forceinline__ void local_argmax(const float (&v)[V], int e0, float&
   bi = e0 + ix;
 }
 
+// local_argmax for values that are never NaN: the max tree in IEEE
+// maximum, which gfx950 issues as v_maximum3_f32 with no canonicalisation of
+// operands (fmaxf quiets each operand not known to be canonical first).  For
+// non-NaN inputs the result and the index are local_argmax's.
+template <int V>
+__device__ __forceinline__ void local_argmax_nn(const float (&v)[V], int e0, float& bv, int& bi) {
+  float m[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) m[j] = v[j];
+  // a ternary tree: each node one three-operand maximum
+#pragma unroll
+  for (int w = V; w > 1; w = (w + 2) / 3)
+#pragma unroll
+    for (int j = 0; j < (w + 2) / 3; ++j) {
+      const float a = m[3 * j];
+      const float b = 3 * j + 1 < w ? m[3 * j + 1] : a;
+      const float c = 3 * j + 2 < w ? m[3 * j + 2] : b;
+      m[j] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+    }
+  bv = m[0];
+  int ix = V - 1;
+#pragma unroll
+  for (int j = V - 2; j >= 0; --j) ix = v[j] == bv ? j : ix;
+  bi = e0 + ix;
+}
+
 constexpr int ilog2c(int v) { return v <= 1 ? 0 : 1 + ilog2c(v / 2); }
 
 // V contiguous floats; 16-byte accesses when V is a multiple of 4 (a lane's
@@ -232,9 +258,11 @@ __device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const floa
         t2[n] = NEG_INF;
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-          // running top two, as selects: (t1, t2) <- top2(t1, t2, v)
-          t2[n] = fmaxf(t2[n], fminf(t1[n], sel[n][j]));
-          t1[n] = fmaxf(t1[n], sel[n][j]);
+          // running top two: (t1, t2) <- top2(t1, t2, v).  sel is never NaN
+          // (det_sigmoid clamps its argument), so IEEE maximum / minimum give
+          // fmaxf / fminf's values without canonicalising the operands
+          t2[n] = __builtin_elementwise_maximum(t2[n], __builtin_elementwise_minimum(t1[n], sel[n][j]));
+          t1[n] = __builtin_elementwise_maximum(t1[n], sel[n][j]);
         }
       }
       MOE_FOR_LEVELS(0, lgl, {
@@ -322,14 +350,17 @@ __device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const floa
       for (int j = 0; j < V; ++j) {
         const float a = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(sel[0][j])));
         const float d = __int_as_float(__builtin_amdgcn_ds_bpermute(addr, __float_as_int(sel[1][j])));
-        cs[j] = has ? (half ? d : a) : NEG_INF;
+        // canonical once here, so the rounds' max trees need no per-use
+        // canonicalisation (a value that came through an integer move is
+        // not known to be)
+        cs[j] = has ? __builtin_canonicalizef(half ? d : a) : NEG_INF;
       }
 #pragma unroll
       for (int r = 0; r < (KK > 0 ? KK : 8); ++r) {
         if (KK == 0 && r >= k) break;
         float bv;
         int bi;
-        local_argmax<V>(cs, ce0, bv, bi);
+        local_argmax_nn<V>(cs, ce0, bv, bi);
         MOE_FOR_LEVELS(0, 2, {
           const float ov = partner_f<L_>(bv);
           const int oi = partner_i<L_>(bi);
@@ -346,8 +377,9 @@ __device__ __forceinline__ void score_tokens(const float (&l)[NT][V], const floa
         my_id[1] = gl == r ? i1 : my_id[1];
         my_sel[0] = gl == r ? v0 : my_sel[0];
         my_sel[1] = gl == r ? v1 : my_sel[1];
+        const int wj = bi - ce0;  // the winner's place in this lane's group, if it is here
 #pragma unroll
-        for (int j = 0; j < V; ++j) cs[j] = ce0 + j == bi ? NEG_INF : cs[j];
+        for (int j = 0; j < V; ++j) cs[j] = j == wj ? NEG_INF : cs[j];
       }
     }
   }
