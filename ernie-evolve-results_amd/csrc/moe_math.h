@@ -28,7 +28,9 @@ __device__ __forceinline__ float det_exp_core(float x) {
   const float LN2_HI = 0x1.62e4p-1f;
   const float LN2_LO = 0x1.7f7d1cp-20f;
   const float k = rintf(x * LOG2E);
-  float r = x - k * LN2_HI;
+  // k * LN2_HI is exact (|k| < 2^9, LN2_HI has 15 significant bits), so the
+  // fused multiply-add rounds once, exactly as x - k * LN2_HI does
+  float r = __builtin_fmaf(-k, LN2_HI, x);
   r = r - k * LN2_LO;
   float p = 0x1.a01a02p-13f;  // 1/7!
   p = p * r + 0x1.6c16c2p-10f;
