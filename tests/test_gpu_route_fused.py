@@ -107,3 +107,40 @@ def test_fused_route_workspace_and_repeat(cuda, E, H):
                      M._ptr(outs[0][0]), M._ptr(outs[0][1]), M._ptr(outs[0][2]), None,
                      M._ptr(ws), nws - 256, M._stream(x))
     assert rc == -4  # MOE_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("topk_group", [1, 2, 3, 4])
+@pytest.mark.parametrize("k", [8, 6])
+def test_fused_sigmoid_group_ties_and_kept_group_counts(cuda, topk_group, k):
+    """E = 256 in 8 groups of 32 (one scoring lane per group, two tokens per
+    lane group: the epilogue ranks only the kept groups, compacted into the
+    lane group).  Router rows repeat every 37 experts and the bias every 37
+    entries, so many scores tie exactly, inside a group and across groups;
+    ties go to the lower expert index.  The fused kernel must select what
+    the one-token scoring kernel and the oracle select on the same logits,
+    for 1 to 4 kept groups."""
+    E, H, T = 256, 7168, 300
+    cfg = RouteCfg(SCORING_SIGMOID_GROUP, True, 8, topk_group, 2.5)
+    g = torch.Generator().manual_seed(100 + 10 * topk_group + k)
+    x = torch.randn(T, H, generator=g).bfloat16()
+    base = (torch.randn(37, H, generator=g) * 0.02).bfloat16()
+    w = base[torch.arange(E) % 37].contiguous()
+    bias = (torch.randn(37, generator=g) * 0.1)[torch.arange(E) % 37].contiguous()
+    x, w, bias = x.to(cuda), w.to(cuda), bias.to(cuda)
+    lf, idf, wf, cf = M.route(x, w, bias, k, cfg)
+    lo, ido, wo, co = two_kernel_route(x, w, bias, k, cfg)
+    torch.cuda.synchronize()
+    print("ties topk_group=%d k=%d" % (topk_group, k), flush=True)
+    assert torch.equal(lf, lo)
+    # exact ties are present: expert e and e + 37 have equal logits
+    assert torch.equal(lf[:, 0], lf[:, 37])
+    assert torch.equal(idf, ido)
+    assert torch.equal(wf, wo)
+    assert torch.equal(cf, co)
+    ocfg = O.RouteCfg(cfg.scoring, cfg.renormalize, cfg.n_group, cfg.topk_group,
+                      cfg.route_scale, cfg.norm_min)
+    oi, ow = O.score_topk(lf.cpu().numpy(), bias.cpu().numpy(), k, ocfg)
+    assert np.array_equal(idf.cpu().numpy(), oi)
+    # every selected expert lies in one of the token's topk_group kept groups
+    groups = idf.cpu().numpy() // 32
+    assert all(len(set(r)) <= topk_group for r in groups)
