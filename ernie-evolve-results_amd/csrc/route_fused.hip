@@ -1,5 +1,5 @@
-// Stages 1+2 in one kernel at E = 256: router GEMM + scoring + top-k +
-// histogram, with the logits tile kept on chip.
+// Stages 1+2 in one kernel at E = 256 and E = 128: router GEMM + scoring +
+// top-k + histogram, with the logits tile kept on chip.
 //
 // Replaces the reference's cublasGemmEx (K:4327-4339) followed by
 // topk_kernel (K:1829-1920), which writes the [T,E] fp32 logits to HBM and
@@ -24,12 +24,14 @@
 //               other.  Rows past T read as zeros (buffer bounds).
 //   epilogue    the BM x E fp32 tile goes through LDS once; its rows are
 //               copied out to router_logits (1 KB per wavefront store,
-//               non-temporal), then 8 lanes per token (16 at E = 128) score
-//               it with the scoring kernel's per-token routine (bit-identical
-//               selection) and write the ids and weights and the block's
-//               expert histogram -- optionally one per 256 (token,
-//               slot) pairs, the permute's block histograms, so the permute
-//               needs no histogram pass.
+//               non-temporal), then 8 lanes per token (32 experts each at
+//               E = 256, 16 at E = 128) score it with the scoring kernel's
+//               per-token routine (bit-identical selection; at E = 256 two
+//               tokens per 8 lanes, whose kept expert groups the selection
+//               rounds compact into the 8 lanes) and write the ids and
+//               weights and the block's expert histogram -- optionally one
+//               per 256 (token, slot) pairs, the permute's block histograms,
+//               so the permute needs no histogram pass.
 #include <utility>
 
 #include "moe_common.h"
@@ -420,8 +422,10 @@ __global__ void rf_zero_kernel(int* __restrict__ p, int n) {
   if (i < n) p[i] = 0;
 }
 
-// The configurations shipped (rf::Cfg): 8 waves (two per SIMD), one token per
-// lane group per scoring pass, the K loop fully unrolled:
+// The configurations shipped (rf::Cfg): 8 waves (two per SIMD; one wave per
+// SIMD with 128 x 64 wave tiles ran the same K loop time and a slower
+// scoring), the K loop fully unrolled, two tokens per lane group per scoring
+// pass at E = 256 and one at E = 128:
 //   E = 256, H = 7168 (DeepSeek-V3): 128-token tiles, 112 K steps, 4 x-ring
 //                                    stages of 32 KB, weights 5 steps ahead;
 //   E = 128, H = 2048 (Qwen3-MoE):   64-token tiles (256 of them at T = 16384),
