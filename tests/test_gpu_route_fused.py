@@ -109,16 +109,17 @@ def test_fused_route_workspace_and_repeat(cuda, E, H):
     assert rc == -4  # MOE_ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("topk_group", [1, 2, 3, 4])
+@pytest.mark.parametrize("topk_group", [1, 2, 3, 4, 6, 8])
 @pytest.mark.parametrize("k", [8, 6])
 def test_fused_sigmoid_group_ties_and_kept_group_counts(cuda, topk_group, k):
     """E = 256 in 8 groups of 32 (one scoring lane per group, two tokens per
-    lane group: the epilogue ranks only the kept groups, compacted into the
-    lane group).  Router rows repeat every 37 experts and the bias every 37
-    entries, so many scores tie exactly, inside a group and across groups;
-    ties go to the lower expert index.  The fused kernel must select what
-    the one-token scoring kernel and the oracle select on the same logits,
-    for 1 to 4 kept groups."""
+    lane group: with at most 4 kept groups the epilogue ranks only those,
+    compacted into the lane group; with more it ranks all 8 lanes).  Router
+    rows repeat every 37 experts and the bias every 37 entries, so many
+    scores tie exactly, inside a group and across groups; ties go to the
+    lower expert index.  The fused kernel must select what the one-token
+    scoring kernel and the oracle select on the same logits, for 1 to 8
+    kept groups."""
     E, H, T = 256, 7168, 300
     cfg = RouteCfg(SCORING_SIGMOID_GROUP, True, 8, topk_group, 2.5)
     g = torch.Generator().manual_seed(100 + 10 * topk_group + k)
